@@ -1,0 +1,355 @@
+/*
+ * ggml_cpu_ref.c - CPU oracle (test infrastructure; see ggml_cpu_ref.h).
+ *
+ * Built with -ffp-contract=off so that every multiply and add rounds on its
+ * own, as ggml's scalar reference code does; where ggml's x86 kernels use a
+ * fused multiply-add (ggml_vec_mad_f32) the code calls fmaf explicitly.
+ */
+#include "ggml_cpu_ref.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ---------------------------------------------------------------- fp16 --- */
+
+uint16_t orc_fp32_to_fp16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu)); /* NaN */
+    if (ax >= 0x47800000u) return (uint16_t)(sign | 0x7c00u); /* >= 65536: inf */
+    if (ax >= 0x38800000u) {                                  /* normal in fp16 */
+        const uint32_t e = (ax >> 23) - 127 + 15;
+        const uint32_t m = ax & 0x7fffffu;
+        uint32_t r = (e << 10) | (m >> 13);
+        const uint32_t rem = m & 0x1fffu;
+        if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r += 1; /* may carry into inf */
+        return (uint16_t)(sign | r);
+    }
+    if (ax <= 0x33000000u) return (uint16_t)sign; /* <= 2^-25 rounds to zero (tie -> even 0) */
+    /* fp16 subnormal: value / 2^-24 rounded to nearest even */
+    const uint32_t E = ax >> 23;
+    const uint32_t M = (ax & 0x7fffffu) | 0x800000u;
+    const uint32_t s = 126 - E; /* 14..24 */
+    uint32_t r = M >> s;
+    const uint32_t rem = M & ((1u << s) - 1u);
+    const uint32_t half = 1u << (s - 1);
+    if (rem > half || (rem == half && (r & 1u))) r += 1;
+    return (uint16_t)(sign | r);
+}
+
+float orc_fp16_to_fp32(uint16_t h) {
+    const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu;
+    const uint32_t m = h & 0x3ffu;
+    uint32_t x;
+    if (e == 0) {
+        if (m == 0) {
+            x = sign;
+        } else { /* subnormal: normalise */
+            float v = (float)m * 5.9604644775390625e-08f; /* m * 2^-24, exact */
+            memcpy(&x, &v, 4);
+            x |= sign;
+        }
+    } else if (e == 31) {
+        x = sign | 0x7f800000u | (m << 13);
+    } else {
+        x = sign | ((e - 15 + 127) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+/* ---------------------------------------------------------------- q4_0 --- */
+
+/* ggml quantize_row_q4_0_ref: d = max / -8 where max is the signed value of
+ * largest magnitude (first occurrence wins: strict `<`), id = 1/d, code =
+ * min(15, (int8_t)(x*id + 8.5f)) with the product and the add rounded
+ * separately; d is stored as fp16 but the codes use the fp32 d. */
+void orc_quantize_row_q4_0(const float *x, uint8_t *y, int64_t k) {
+    const int qk = SQA_QK4_0;
+    const int64_t nb = k / qk;
+    for (int64_t i = 0; i < nb; i++) {
+        float amax = 0.0f;
+        float max = 0.0f;
+        for (int j = 0; j < qk; j++) {
+            const float v = x[i * qk + j];
+            if (amax < fabsf(v)) {
+                amax = fabsf(v);
+                max = v;
+            }
+        }
+        const float d = max / -8;
+        const float id = d ? 1.0f / d : 0.0f;
+        uint8_t *blk = y + i * SQA_Q4_0_BLOCK_BYTES;
+        const uint16_t dh = orc_fp32_to_fp16(d);
+        memcpy(blk, &dh, 2);
+        for (int j = 0; j < qk / 2; ++j) {
+            const float x0 = x[i * qk + 0 + j] * id;
+            const float x1 = x[i * qk + qk / 2 + j] * id;
+            const int8_t t0 = (int8_t)(x0 + 8.5f);
+            const int8_t t1 = (int8_t)(x1 + 8.5f);
+            const uint8_t xi0 = (uint8_t)(t0 < 15 ? t0 : 15);
+            const uint8_t xi1 = (uint8_t)(t1 < 15 ? t1 : 15);
+            blk[2 + j] = (uint8_t)(xi0 | (xi1 << 4));
+        }
+    }
+}
+
+void orc_dequantize_row_q4_0(const uint8_t *x, float *y, int64_t k) {
+    const int qk = SQA_QK4_0;
+    const int64_t nb = k / qk;
+    for (int64_t i = 0; i < nb; i++) {
+        const uint8_t *blk = x + i * SQA_Q4_0_BLOCK_BYTES;
+        uint16_t dh;
+        memcpy(&dh, blk, 2);
+        const float d = orc_fp16_to_fp32(dh);
+        for (int j = 0; j < qk / 2; ++j) {
+            const int x0 = (blk[2 + j] & 0x0F) - 8;
+            const int x1 = (blk[2 + j] >> 4) - 8;
+            y[i * qk + j + 0] = x0 * d;
+            y[i * qk + j + qk / 2] = x1 * d;
+        }
+    }
+}
+
+/* ---------------------------------------------------------------- q8_0 --- */
+
+void orc_quantize_row_q8_0(const float *x, uint8_t *y, int64_t k, int variant) {
+    const int qk = 32;
+    const int64_t nb = k / qk;
+    for (int64_t i = 0; i < nb; i++) {
+        float amax = 0.0f;
+        for (int j = 0; j < qk; j++) {
+            const float a = fabsf(x[i * qk + j]);
+            amax = amax > a ? amax : a;
+        }
+        uint8_t *blk = y + i * ORC_Q8_0_BLOCK_BYTES;
+        int8_t *qs = (int8_t *)(blk + 2);
+        const float d = amax / 127.f;
+        const uint16_t dh = orc_fp32_to_fp16(d);
+        memcpy(blk, &dh, 2);
+        if (variant == ORC_Q8_X86) {
+            const float id = (amax != 0.0f) ? 127.f / amax : 0.0f;
+            for (int j = 0; j < qk; j++) qs[j] = (int8_t)nearbyintf(x[i * qk + j] * id);
+        } else {
+            const float id = d ? 1.0f / d : 0.0f;
+            for (int j = 0; j < qk; j++) qs[j] = (int8_t)roundf(x[i * qk + j] * id);
+        }
+    }
+}
+
+/* q4_0 . q8_0: per block the exact integer sum of (nib-8)*q8, scaled by
+ * d4 * d8 and accumulated in fp32 (ggml's scalar vec_dot order). */
+float orc_vec_dot_q4_0_q8_0(int64_t n, const uint8_t *x, const uint8_t *y) {
+    const int64_t nb = n / 32;
+    float sumf = 0.0f;
+    for (int64_t ib = 0; ib < nb; ++ib) {
+        const uint8_t *bx = x + ib * SQA_Q4_0_BLOCK_BYTES;
+        const uint8_t *by = y + ib * ORC_Q8_0_BLOCK_BYTES;
+        const int8_t *qy = (const int8_t *)(by + 2);
+        int sumi0 = 0, sumi1 = 0;
+        for (int j = 0; j < 16; ++j) {
+            const int v0 = (bx[2 + j] & 0x0F) - 8;
+            const int v1 = (bx[2 + j] >> 4) - 8;
+            sumi0 += v0 * qy[j];
+            sumi1 += v1 * qy[j + 16];
+        }
+        const int sumi = sumi0 + sumi1;
+        uint16_t dx, dy;
+        memcpy(&dx, bx, 2);
+        memcpy(&dy, by, 2);
+        sumf += (float)sumi * orc_fp16_to_fp32(dx) * orc_fp16_to_fp32(dy);
+    }
+    return sumf;
+}
+
+/* ------------------------------------------------------------ set_rows --- */
+
+int orc_set_rows_q4_0(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *idx) {
+    if (!dst || !src || !idx) return SQA_ERR_INVALID;
+    if (dst->type != SQA_TYPE_Q4_0 || src->type != SQA_TYPE_F32 || idx->type != SQA_TYPE_I64)
+        return SQA_ERR_INVALID;
+    const int64_t ne0 = src->ne[0];
+    const int64_t n_rows = src->ne[1];
+    if (dst->ne[0] != ne0 || ne0 % SQA_QK4_0 != 0 || idx->ne[0] != n_rows) return SQA_ERR_INVALID;
+    for (int64_t i = 0; i < n_rows; ++i) {
+        const int64_t r = *(const int64_t *)((const char *)idx->data + i * idx->nb[0]);
+        if (r < 0 || r >= dst->ne[1]) continue; /* ggml asserts; the device kernel skips */
+        orc_quantize_row_q4_0((const float *)((const char *)src->data + i * src->nb[1]),
+                              (uint8_t *)dst->data + r * dst->nb[1], ne0);
+    }
+    return SQA_OK;
+}
+
+/* -------------------------------------------------------- flash attention --- */
+
+/* One (query, head) row of ggml's CPU flash_attn_ext: Q row -> q8_0, then for
+ * every key with a mask value other than -inf: s = scale * (q4_0 . q8_0) (+
+ * softcap) + slope*mask; online softmax with expf; V dequantised to fp32 and
+ * accumulated with a fused multiply-add; finally divided by the sum (0 if the
+ * sum is 0, i.e. every key masked). causal_limit >= 0 replaces the mask with
+ * "key <= causal_limit". */
+static void fa_row(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
+                   const sqa_tensor *mask, int64_t causal_limit, float scale, float slope,
+                   float logit_softcap, int64_t iq1, int64_t iq2, float *out, float *vkq,
+                   float *v32, uint8_t *q_q, int q8_variant) {
+    const int64_t DK = k->ne[0];
+    const int64_t DV = v->ne[0];
+    const int64_t n_kv = k->ne[1];
+    const int64_t rk2 = q->ne[2] / k->ne[2];
+    const int64_t rv2 = q->ne[2] / v->ne[2];
+    const int64_t ik2 = iq2 / rk2;
+    const int64_t iv2 = iq2 / rv2;
+
+    const float *pq = (const float *)((const char *)q->data + iq1 * q->nb[1] + iq2 * q->nb[2]);
+    orc_quantize_row_q8_0(pq, q_q, DK, q8_variant);
+    const uint16_t *mp =
+        mask ? (const uint16_t *)((const char *)mask->data + iq1 * mask->nb[1]) : NULL;
+
+    float S = 0.0f;
+    float M = -INFINITY;
+    memset(vkq, 0, DV * sizeof(float));
+    for (int64_t ic = 0; ic < n_kv; ++ic) {
+        float mv;
+        if (causal_limit >= 0) {
+            mv = ic <= causal_limit ? 0.0f : -INFINITY;
+        } else {
+            mv = mp ? slope * orc_fp16_to_fp32(mp[ic]) : 0.0f;
+        }
+        if (mv == -INFINITY) continue;
+
+        const uint8_t *kd = (const uint8_t *)k->data + ic * k->nb[1] + ik2 * k->nb[2];
+        float s = orc_vec_dot_q4_0_q8_0(DK, kd, q_q);
+        s = s * scale;
+        if (logit_softcap != 0.0f) s = logit_softcap * tanhf(s);
+        s += mv;
+
+        const float Mold = M;
+        float ms = 1.0f;
+        float vs = 1.0f;
+        if (s > M) {
+            M = s;
+            ms = expf(Mold - M);
+            for (int64_t d = 0; d < DV; ++d) vkq[d] *= ms;
+        } else {
+            vs = expf(s - M);
+        }
+        const uint8_t *vd = (const uint8_t *)v->data + ic * v->nb[1] + iv2 * v->nb[2];
+        orc_dequantize_row_q4_0(vd, v32, DV);
+        for (int64_t d = 0; d < DV; ++d) vkq[d] = fmaf(v32[d], vs, vkq[d]);
+        S = S * ms + vs;
+    }
+    const float S_inv = S == 0.0f ? 0.0f : 1.0f / S;
+    for (int64_t d = 0; d < DV; ++d) out[d] = vkq[d] * S_inv;
+}
+
+static int fa_check(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
+                    const sqa_tensor *mask, const sqa_tensor *dst) {
+    if (!q || !k || !v || !dst) return SQA_ERR_INVALID;
+    if (q->type != SQA_TYPE_F32 || k->type != SQA_TYPE_Q4_0 || v->type != SQA_TYPE_Q4_0 ||
+        dst->type != SQA_TYPE_F32)
+        return SQA_ERR_INVALID;
+    if (q->ne[0] != k->ne[0] || k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2]) return SQA_ERR_INVALID;
+    if (q->ne[0] % SQA_QK4_0 || v->ne[0] % SQA_QK4_0) return SQA_ERR_INVALID;
+    if (k->ne[2] <= 0 || q->ne[2] % k->ne[2]) return SQA_ERR_INVALID;
+    if (dst->ne[0] != v->ne[0] || dst->ne[1] != q->ne[2] || dst->ne[2] != q->ne[1])
+        return SQA_ERR_INVALID;
+    if (q->ne[3] != 1 || k->ne[3] != 1) return SQA_ERR_UNSUPPORTED;
+    if (mask) {
+        if (mask->type != SQA_TYPE_F16 || mask->ne[0] != k->ne[1] || mask->ne[1] < q->ne[1])
+            return SQA_ERR_INVALID;
+    }
+    return SQA_OK;
+}
+
+static int fa_run(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
+                  const sqa_tensor *mask, int64_t q_pos0, const sqa_tensor *gate, float scale,
+                  float max_bias, float logit_softcap, const sqa_tensor *dst, int n_threads,
+                  int q8_variant) {
+    const int64_t n_q = q->ne[1];
+    const int64_t H = q->ne[2];
+    const int64_t DK = k->ne[0];
+    const int64_t DV = v->ne[0];
+    const int64_t n_rows = n_q * H;
+    if (logit_softcap != 0.0f) scale /= logit_softcap;
+    const uint32_t n_head_log2 = 1u << (uint32_t)floor(log2((double)H));
+    const float m0 = powf(2.0f, -(max_bias) / n_head_log2);
+    const float m1 = powf(2.0f, -(max_bias / 2.0f) / n_head_log2);
+    if (n_threads < 1) n_threads = 1;
+
+#pragma omp parallel num_threads(n_threads)
+    {
+        float *vkq = (float *)malloc(DV * sizeof(float));
+        float *v32 = (float *)malloc(DV * sizeof(float));
+        uint8_t *q_q = (uint8_t *)malloc((DK / 32) * ORC_Q8_0_BLOCK_BYTES);
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t ir = 0; ir < n_rows; ++ir) {
+            const int64_t iq2 = ir / n_q; /* head */
+            const int64_t iq1 = ir % n_q; /* query */
+            const uint32_t h = (uint32_t)iq2;
+            const float slope = (max_bias > 0.0f)
+                                    ? (h < n_head_log2 ? powf(m0, h + 1)
+                                                       : powf(m1, 2 * (h - n_head_log2) + 1))
+                                    : 1.0f;
+            float *out = (float *)((char *)dst->data + (iq1 * H + iq2) * DV * sizeof(float));
+            const int64_t climit = q_pos0 >= 0 ? q_pos0 + iq1 : -1;
+            fa_row(q, k, v, mask, climit, scale, slope, logit_softcap, iq1, iq2, out, vkq, v32,
+                   q_q, q8_variant);
+            if (gate) {
+                const float *g =
+                    (const float *)((const char *)gate->data + iq1 * gate->nb[2] + iq2 * gate->nb[1]);
+                for (int64_t d = 0; d < DV; ++d) out[d] = out[d] * (1.f / (1.f + expf(-g[d])));
+            }
+        }
+        free(vkq);
+        free(v32);
+        free(q_q);
+    }
+    return SQA_OK;
+}
+
+int orc_flash_attn_ext(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
+                       const sqa_tensor *mask, float scale, float max_bias, float logit_softcap,
+                       const sqa_tensor *dst, int n_threads, int q8_variant) {
+    const int rc = fa_check(q, k, v, mask, dst);
+    if (rc) return rc;
+    return fa_run(q, k, v, mask, -1, NULL, scale, max_bias, logit_softcap, dst, n_threads,
+                  q8_variant);
+}
+
+int orc_flash_attn_ext_causal(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
+                              int64_t q_pos0, const sqa_tensor *gate, float scale,
+                              const sqa_tensor *dst, int n_threads, int q8_variant) {
+    const int rc = fa_check(q, k, v, NULL, dst);
+    if (rc) return rc;
+    if (q_pos0 < 0) return SQA_ERR_RANGE;
+    return fa_run(q, k, v, NULL, q_pos0, gate, scale, 0.0f, 0.0f, dst, n_threads, q8_variant);
+}
+
+/* ggml_vec_sigmoid_f32 (1/(1+expf(-x))) followed by ggml_mul. */
+int orc_sigmoid_mul(const sqa_tensor *dst, const sqa_tensor *x, const sqa_tensor *gate) {
+    if (!dst || !x || !gate) return SQA_ERR_INVALID;
+    const int64_t n0 = x->ne[0], n1 = x->ne[1];
+    for (int64_t j = 0; j < n1; ++j) {
+        const float *xr = (const float *)((const char *)x->data + j * x->nb[1]);
+        const float *gr = (const float *)((const char *)gate->data + j * gate->nb[1]);
+        float *dr = (float *)((char *)dst->data + j * dst->nb[1]);
+        for (int64_t i = 0; i < n0; ++i) dr[i] = xr[i] * (1.f / (1.f + expf(-gr[i])));
+    }
+    return SQA_OK;
+}
+
+int orc_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

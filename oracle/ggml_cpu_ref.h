@@ -1,0 +1,70 @@
+/*
+ * ggml_cpu_ref.h - CPU oracle for the full-attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This is the checker the HIP kernels are compared
+ * against: only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline
+ * leg may load it. The product library never links or calls it.
+ *
+ * It restates, from the published algorithm, ggml's CPU-backend semantics for
+ * the ops the engine issues on this path. ggml itself is an external
+ * dependency of the reference (llama.cpp commit ed7ac35e1, named at
+ * src/backend/ffi.rs:1 of the reference), not vendored and not present here.
+ * Functions and the reference call sites they follow:
+ *   orc_fp32_to_fp16 / orc_fp16_to_fp32  - IEEE binary16, round-to-nearest-even
+ *                                          (f16_to_f32 of tests/kernel_verify.rs:253-268)
+ *   orc_quantize_row_q4_0                - ggml quantize_row_q4_0_ref (the quantizer the
+ *                                          tests call through ggml_quantize_chunk,
+ *                                          tests/attn_test.rs:210-229; rules at :781-788)
+ *   orc_dequantize_row_q4_0              - tests/kernel_verify.rs:270-292, attn_test.rs:257-276
+ *   orc_quantize_row_q8_0                - ggml's q8_0 from_float, the vec_dot type of q4_0
+ *   orc_vec_dot_q4_0_q8_0                - ggml's q4_0 x q8_0 block dot
+ *   orc_set_rows_q4_0                    - GGML_OP_SET_ROWS CPU loop (src/engine/kv.rs:313-399)
+ *   orc_flash_attn_ext                   - ggml CPU flash_attn_ext one-chunk online softmax,
+ *                                          the op built at src/model/attn.rs:228-251
+ *   orc_flash_attn_ext_causal            - the same with the causal rule of
+ *                                          src/model/graph.rs:486-576 and the gate of
+ *                                          src/model/attn.rs:282-283
+ *   orc_sigmoid_mul                      - ggml_sigmoid + ggml_mul (src/model/attn.rs:282-283)
+ */
+#ifndef GGML_CPU_REF_H
+#define GGML_CPU_REF_H
+
+#include <stdint.h>
+#include "../include/sqattn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORC_Q8_0_BLOCK_BYTES 34
+
+/* Q -> q8_0 rounding variants: ggml's x86 (AVX2) from_float uses id = 127/amax
+ * and round-to-nearest-even; its portable scalar reference uses id = 1/d and
+ * roundf (ties away from zero). */
+#define ORC_Q8_X86 0
+#define ORC_Q8_SCALAR 1
+
+uint16_t orc_fp32_to_fp16(float f);
+float orc_fp16_to_fp32(uint16_t h);
+
+void orc_quantize_row_q4_0(const float *x, uint8_t *y, int64_t k);
+void orc_dequantize_row_q4_0(const uint8_t *x, float *y, int64_t k);
+void orc_quantize_row_q8_0(const float *x, uint8_t *y, int64_t k, int variant);
+float orc_vec_dot_q4_0_q8_0(int64_t n, const uint8_t *x, const uint8_t *y);
+
+/* Host-memory versions of the C-ABI ops (same descriptors, host pointers). */
+int orc_set_rows_q4_0(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *idx);
+int orc_flash_attn_ext(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
+                       const sqa_tensor *mask, float scale, float max_bias, float logit_softcap,
+                       const sqa_tensor *dst, int n_threads, int q8_variant);
+int orc_flash_attn_ext_causal(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
+                              int64_t q_pos0, const sqa_tensor *gate, float scale,
+                              const sqa_tensor *dst, int n_threads, int q8_variant);
+int orc_sigmoid_mul(const sqa_tensor *dst, const sqa_tensor *x, const sqa_tensor *gate);
+
+int orc_max_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

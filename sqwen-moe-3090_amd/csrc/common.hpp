@@ -1,0 +1,49 @@
+// common.hpp - shared definitions of the gfx950 attention library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/sqattn.h"
+
+namespace sqa {
+
+// Head dimension and q4_0 geometry of the path (qwen35moe full attention:
+// head_dim 256 enforced at src/model/arch.rs:156-160 of the reference).
+constexpr int kHeadDim = 256;
+constexpr int kBlocksPerHead = kHeadDim / SQA_QK4_0;            // 8
+constexpr int kHeadRowBytes = kBlocksPerHead * SQA_Q4_0_BLOCK_BYTES;  // 144
+
+// Records a message for sqa_last_error() and returns the status.
+int set_error(int status, const char *fmt, ...);
+int hip_status(hipError_t e, const char *what);
+
+// Device count of compute units (cached per device).
+int device_cu_count();
+
+// Optional event timing around launches (profile.cpp).
+bool profile_on();
+int profile_start(const char *name, hipStream_t s);
+void profile_stop(int slot, hipStream_t s);
+
+// Kernel launchers (defined next to their kernels).
+int launch_set_rows_q4_0(const sqa_tensor &dst, const sqa_tensor &src, const sqa_tensor &idx,
+                         hipStream_t s);
+int launch_sigmoid_mul(const sqa_tensor &dst, const sqa_tensor &x, const sqa_tensor &gate,
+                       hipStream_t s);
+int launch_fill_causal_mask(const sqa_tensor &mask, int64_t step_start, hipStream_t s);
+
+struct FaArgs {
+    const sqa_tensor *q, *k, *v, *mask, *gate, *dst;
+    float scale;
+    int64_t q_pos0;  // >= 0: causal from positions, mask ignored
+    void *ws;
+    size_t ws_bytes;
+};
+size_t fa_decode_workspace(int64_t n_q, int64_t H, int64_t n_kv);
+int launch_fa_decode(const FaArgs &a, hipStream_t s);
+size_t fa_prefill_workspace(int64_t n_q, int64_t H, int64_t n_kv);
+int launch_fa_prefill(const FaArgs &a, hipStream_t s);
+
+}  // namespace sqa

@@ -1,0 +1,104 @@
+"""Split-KV decode / verify flash_attn_ext on the GPU against the oracle's ggml
+CPU flash_attn_ext on identical inputs. Tolerance (stated by the spec of this
+path): max |gpu - oracle| <= 2e-3 * rms(oracle)."""
+import numpy as np
+import pytest
+import torch
+
+from tests.gen import qkv, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def run_gpu(sqa, dev, q, kq, vq, mask=None, causal=None, gate=None, scale=1 / 16):
+    qt = torch.from_numpy(q).to(dev)
+    kt = torch.from_numpy(np.ascontiguousarray(kq)).to(dev)
+    vt = torch.from_numpy(np.ascontiguousarray(vq)).to(dev)
+    n_kv = kq.shape[0]
+    if causal is None:
+        mt = torch.from_numpy(mask).to(dev) if mask is not None else None
+        out = sqa.flash_attn_ext(qt, kt, vt, n_kv, mask=mt, scale=scale)
+    else:
+        gt = torch.from_numpy(gate).to(dev) if gate is not None else None
+        out = sqa.flash_attn_ext_causal(qt, kt, vt, n_kv, causal, gate=gt, scale=scale)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def test_decode_4096_outliers(sqa, orc, dev):
+    """n_q=1, 16q/2kv, hd256, n_kv 4096, 1% of the 512 K/V channels x8."""
+    q, kq, vq = qkv(orc, 1, 1, 4096, outliers=5)
+    mask = orc.causal_mask(1, 4096, 4095)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    err = rel_err(got, ref)
+    print(f"decode n_kv=4096 outliers: max err / rms = {err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("n_kv,start", [(1, 0), (17, 16), (256, 200), (300, 299), (1000, 999), (5000, 4100)])
+def test_decode_ragged_lengths(sqa, orc, dev, n_kv, start):
+    q, kq, vq = qkv(orc, n_kv, 1, n_kv)
+    mask = orc.causal_mask(1, n_kv, start)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("n_kv", [512, 32768])
+def test_verify_two_rows_causal(sqa, orc, dev, n_kv):
+    """MTP verify: n_q=2, row 0 sees n_kv-1 keys, row 1 sees n_kv (graph.rs:554-560)."""
+    q, kq, vq = qkv(orc, 7, 2, n_kv)
+    mask = orc.causal_mask(2, n_kv, n_kv - 2)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    err = rel_err(got, ref)
+    print(f"verify n_kv={n_kv}: max err / rms = {err:.3e}")
+    assert err <= TOL
+
+
+def test_finite_mask_values_and_fully_masked_row(sqa, orc, dev):
+    q, kq, vq = qkv(orc, 11, 2, 700)
+    rng = np.random.default_rng(12)
+    mask = (-rng.uniform(0, 3, (2, 700))).astype(np.float16)
+    mask[0, rng.choice(700, 200, replace=False)] = -np.inf
+    mask[1, :] = -np.inf
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    assert np.all(got[1] == 0)
+    assert rel_err(got[0], ref[0]) <= TOL
+
+
+def test_no_mask_and_other_scale(sqa, orc, dev):
+    q, kq, vq = qkv(orc, 13, 1, 2048)
+    ref = orc.flash_attn_ext(q, kq, vq, None, scale=0.1)
+    got = run_gpu(sqa, dev, q, kq, vq, None, scale=0.1)
+    assert rel_err(got, ref) <= TOL
+
+
+def test_causal_positions_with_fused_gate(sqa, orc, dev):
+    q, kq, vq = qkv(orc, 17, 2, 4096)
+    gate = np.random.default_rng(18).standard_normal(q.shape).astype(np.float32)
+    ref = orc.flash_attn_ext_causal(q, kq, vq, 3000, gate=gate)
+    got = run_gpu(sqa, dev, q, kq, vq, causal=3000, gate=gate)
+    assert rel_err(got, ref) <= TOL
+
+
+def test_decode_is_deterministic(sqa, orc, dev):
+    q, kq, vq = qkv(orc, 19, 1, 20000)
+    a = run_gpu(sqa, dev, q, kq, vq)
+    b = run_gpu(sqa, dev, q, kq, vq)
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("n_q,n_kv", [(1, 172032), (2, 131072)])
+def test_full_size_against_oracle(sqa, orc, dev, n_q, n_kv):
+    """Decode at 172K context and verify at 128K, the long-context shapes."""
+    q, kq, vq = qkv(orc, 23 + n_q, n_q, n_kv)
+    mask = orc.causal_mask(n_q, n_kv, n_kv - n_q)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    err = rel_err(got, ref)
+    print(f"n_q={n_q} n_kv={n_kv}: max err / rms = {err:.3e}")
+    assert err <= TOL
