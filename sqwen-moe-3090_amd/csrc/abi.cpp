@@ -94,6 +94,8 @@ int check_fa(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
     *decode = q->ne[1] * G <= 16;
     if (*decode && k->ne[2] != 2)
         return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: decode kernel needs n_head_kv == 2");
+    if (*decode && ((uintptr_t)q->data % 16 || q->nb[1] % 16 || q->nb[2] % 16))
+        return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: q rows must be 16-byte aligned");
     if (!*decode)
         return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: prefill (n_q*g > 16) not built yet");
     return SQA_OK;
@@ -113,6 +115,7 @@ int check_mask(const sqa_tensor *mask, const sqa_tensor *q, const sqa_tensor *k)
         return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: mask rows must be contiguous");
     if (mask->ne[2] != 1 || mask->ne[3] != 1)
         return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: per-head masks not supported");
+
     return SQA_OK;
 }
 
