@@ -96,8 +96,8 @@ int check_fa(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
         return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: decode kernel needs n_head_kv == 2");
     if (*decode && ((uintptr_t)q->data % 16 || q->nb[1] % 16 || q->nb[2] % 16))
         return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: q rows must be 16-byte aligned");
-    if (!*decode)
-        return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: prefill (n_q*g > 16) not built yet");
+    if (!*decode && 16 % G != 0)
+        return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: prefill needs n_head/n_head_kv to divide 16");
     return SQA_OK;
 }
 
@@ -120,8 +120,8 @@ int check_mask(const sqa_tensor *mask, const sqa_tensor *q, const sqa_tensor *k)
 }
 
 size_t fa_workspace(const sqa_tensor *q, const sqa_tensor *k, bool decode) {
-    const int64_t n_q = q->ne[1], H = q->ne[2], n_kv = k->ne[1];
-    return decode ? fa_decode_workspace(n_q, H, n_kv) : fa_prefill_workspace(n_q, H, n_kv);
+    const int64_t n_q = q->ne[1], H = q->ne[2], n_kv = k->ne[1], Hkv = k->ne[2];
+    return decode ? fa_decode_workspace(n_q, H, n_kv) : fa_prefill_workspace(n_q, H, Hkv, n_kv);
 }
 
 int run_fa(const FaArgs &a, bool decode, hipStream_t s) {

@@ -594,6 +594,20 @@ __global__ __launch_bounds__(256) void fa_combine_kernel(const float *__restrict
     }
 }
 
+}  // namespace
+
+int launch_fa_combine(const float *part_acc, const float *part_ml, int n_splits, int rows_total,
+                      float *dst, const sqa_tensor *gate, int H, hipStream_t s) {
+    const int prof = profile_start("fa_combine", s);
+    fa_combine_kernel<<<dim3((unsigned)rows_total, 16), dim3(256), 0, s>>>(
+        part_acc, part_ml, n_splits, rows_total, dst, gate ? (const char *)gate->data : nullptr,
+        gate ? (int64_t)gate->nb[1] : 0, gate ? (int64_t)gate->nb[2] : 0, H);
+    profile_stop(prof, s);
+    return hip_status(hipGetLastError(), "fa_combine launch");
+}
+
+namespace {
+
 int decode_splits(int64_t n_kv) {
     const int64_t units = (n_kv + 15) / 16;
     int64_t s = (units + 7) / 8;  // at least 128 keys per split
@@ -656,13 +670,8 @@ int launch_fa_decode(const FaArgs &a, hipStream_t s) {
     profile_stop(prof, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_status(e, "fa_decode launch");
-    const char *gate = a.gate ? (const char *)a.gate->data : nullptr;
-    prof = profile_start("fa_combine", s);
-    fa_combine_kernel<<<dim3((unsigned)(n_q * H), 16), dim3(256), 0, s>>>(
-        p.part_acc, p.part_ml, p.n_splits, (int)(n_q * H), (float *)a.dst->data, gate,
-        a.gate ? (int64_t)a.gate->nb[1] : 0, a.gate ? (int64_t)a.gate->nb[2] : 0, (int)H);
-    profile_stop(prof, s);
-    return hip_status(hipGetLastError(), "fa_combine launch");
+    return launch_fa_combine(p.part_acc, p.part_ml, p.n_splits, (int)(n_q * H), (float *)a.dst->data, a.gate,
+                             (int)H, s);
 }
 
 }  // namespace sqa

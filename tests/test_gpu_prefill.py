@@ -1,0 +1,64 @@
+"""MFMA prefill flash_attn_ext on the GPU against the oracle's ggml CPU
+flash_attn_ext on identical inputs (ubatch chunks appended after a cached
+prefix, src/engine/runner.rs:1104-1108 in the reference). Tolerance:
+max |gpu - oracle| <= 2e-3 * rms(oracle)."""
+import numpy as np
+import pytest
+import torch
+
+from tests.gen import qkv, rel_err
+from tests.test_gpu_decode import run_gpu
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+@pytest.mark.parametrize("n_q,n_kv,start", [(3, 256, 200), (64, 1024, 960), (100, 777, 600), (512, 4096, 3584)])
+def test_prefill_causal_mask(sqa, orc, dev, n_q, n_kv, start):
+    q, kq, vq = qkv(orc, n_q + n_kv, n_q, n_kv)
+    mask = orc.causal_mask(n_q, n_kv, start)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    err = rel_err(got, ref)
+    print(f"prefill n_q={n_q} n_kv={n_kv}: max err / rms = {err:.3e}")
+    assert err <= TOL
+
+
+def test_prefill_pp512_after_16k(sqa, orc, dev):
+    """ubatch 512 appended after 16384 cached tokens: 16896 keys, causal."""
+    q, kq, vq = qkv(orc, 4, 512, 16896)
+    mask = orc.causal_mask(512, 16896, 16384)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    err = rel_err(got, ref)
+    print(f"pp512 @16384: max err / rms = {err:.3e}")
+    assert err <= TOL
+
+
+def test_prefill_causal_positions_gate(sqa, orc, dev):
+    q, kq, vq = qkv(orc, 5, 200, 2048)
+    gate = np.random.default_rng(6).standard_normal(q.shape).astype(np.float32)
+    ref = orc.flash_attn_ext_causal(q, kq, vq, 1848, gate=gate)
+    got = run_gpu(sqa, dev, q, kq, vq, causal=1848, gate=gate)
+    assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("H,Hkv,n_q", [(4, 1, 40), (16, 16, 40), (8, 4, 40), (16, 16, 200), (4, 2, 150)])
+def test_prefill_other_gqa_ratios(sqa, orc, dev, H, Hkv, n_q):
+    """G = 1 puts 128 query positions in one workgroup (the mask staging of
+    every position is exercised with n_q = 200)."""
+    q, kq, vq = qkv(orc, H + n_q, n_q, 600, H=H, Hkv=Hkv)
+    mask = orc.causal_mask(n_q, 600, 600 - n_q)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    assert rel_err(got, ref) <= TOL
+
+
+def test_prefill_fully_masked_rows_are_zero(sqa, orc, dev):
+    q, kq, vq = qkv(orc, 9, 32, 512)
+    mask = orc.causal_mask(32, 512, 400)
+    mask[5] = -np.inf
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    assert np.all(got[5] == 0)
+    assert rel_err(got, ref) <= TOL
