@@ -13,7 +13,14 @@ bytes of one layer are n_kv*576 (K+V) + 2*16*256*4 (Q, O) + n_kv*2 (mask).
 
 Prints ONE JSON line (rank 0). Extra fields: per-layer microseconds, the
 roofline of the dominant kernel (fa_decode), the CPU oracle timed on this
-host, and the MTP verify (n_q = 2) marginal cost.
+host, the MTP verify (n_q = 2) marginal cost, and the prefill leg:
+pp512 = a 512-token ubatch appended after 16384 cached tokens (n_kv = 16896,
+causal F16 mask), 10 layers, reported as attention TFLOP/s against the fp16
+MFMA peak. Its FLOPs count QK^T and PV over the keys each query may see:
+4 * head_dim * n_head * sum_i (16384 + i + 1).
+
+--copy-ref appends a plain 256 MiB device copy so that hardware counters of
+the same run can be scaled by a kernel of known traffic.
 """
 import argparse
 import json
@@ -25,6 +32,14 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA, MI355X
+PP_N_Q, PP_START = 512, 16384
+STACK_N_Q, STACK_START = 2048, 131072
+# HBM bytes per fa_decode launch at 172K (n_q = 1), from rocprofv3 counter
+# passes over this script: 2.0 x FETCH_SIZE + 1.0 x WRITE_SIZE (KiB x 1024),
+# the factors taken from a plain 256 MiB copy in the same run
+# (profiles/fa_decode_172k_pp512_hbm_traffic.txt).
+DECODE_TRAFFIC_BYTES = int((2.0 * 49068.9 + 4640.0) * 1024)
 H, HKV, D = 16, 2, 256
 N_LAYERS = 10
 N_KV = 172032
@@ -69,6 +84,119 @@ def time_steps(torch, fn, steps):
     return a.elapsed_time(b)  # ms
 
 
+def prefill_flops(n_q, start, heads=H, head_dim=D):
+    """QK^T + PV multiply-adds (2 flops each) over the visible keys."""
+    keys = n_q * (start + 1) + n_q * (n_q - 1) // 2
+    return 4 * head_dim * heads * keys
+
+
+def prefill_leg(sqa, torch, dev, steps, warmup):
+    """pp512 per layer: set_rows of the 512 new K and V rows into the q4_0
+    cache (positions 16384..16895), then flash_attn_ext over 16896 keys with
+    the causal F16 mask."""
+    n_kv = PP_START + PP_N_Q
+    ks, vs = fill_caches(sqa, torch, dev, N_LAYERS, n_kv, seed=7)
+    qs = [torch.randn((PP_N_Q, H, D), device=dev, dtype=torch.float32) for _ in range(N_LAYERS)]
+    knew = [torch.randn((PP_N_Q, HKV * D), device=dev, dtype=torch.float32) for _ in range(N_LAYERS)]
+    vnew = [torch.randn((PP_N_Q, HKV * D), device=dev, dtype=torch.float32) for _ in range(N_LAYERS)]
+    idx = torch.arange(PP_START, n_kv, device=dev, dtype=torch.int64)
+    mask = torch.empty((PP_N_Q, n_kv), dtype=torch.float16, device=dev)
+    sqa.fill_causal_mask(mask, PP_START)
+    out = torch.empty((PP_N_Q, H, D), dtype=torch.float32, device=dev)
+    ws = torch.empty(sqa.flash_attn_workspace_size(qs[0], ks[0], n_kv), dtype=torch.uint8, device=dev)
+
+    def step():
+        for li in range(N_LAYERS):
+            sqa.set_rows_q4_0(ks[li], knew[li], idx)
+            sqa.set_rows_q4_0(vs[li], vnew[li], idx)
+            sqa.flash_attn_ext(qs[li], ks[li], vs[li], n_kv, mask=mask, out=out, workspace=ws)
+
+    for _ in range(warmup):
+        step()
+    ms = time_steps(torch, step, steps) / steps
+    sqa.profile_begin(steps * N_LAYERS * 4 + 16)
+    time_steps(torch, step, steps)
+    sqa.profile_end()
+    kern = {}
+    for name in ("set_rows_q4_0", "fa_prefill_prep", "fa_prefill", "fa_combine"):
+        t, c = sqa.profile_get(name)
+        if c:
+            kern[name] = round(t / c * 1e3, 2)
+    flops = prefill_flops(PP_N_Q, PP_START)
+    tflops = N_LAYERS * flops / (ms * 1e-3) / 1e12
+    main_tf = flops / (kern["fa_prefill"] * 1e-6) / 1e12
+    del ks, vs, qs, ws, knew, vnew
+    return {"workload": f"pp512: n_q={PP_N_Q} after {PP_START} cached (n_kv={n_kv}), 16q/2kv, hd256, "
+                        f"q4_0 K/V (512 new rows quantized on write), causal F16 mask, {N_LAYERS} layers",
+            "per_layer_us": round(ms * 1e3 / N_LAYERS, 2), "TFLOP/s": round(tflops, 1),
+            "pct_of_mfma_f16_peak": round(100 * tflops / MFMA_F16_PEAK_TFLOPS, 1),
+            "kernels_us": kern,
+            "roofline": {"kernel": "fa_prefill", "bound": "mfma", "achieved": round(main_tf, 1),
+                         "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(main_tf / MFMA_F16_PEAK_TFLOPS, 4), "flops_per_launch": flops}}
+
+
+def stack_leg(sqa, torch, dev, steps, warmup):
+    """The 10-layer attention stack of a long prefill: ubatch 2048 at prior
+    context 131072 (n_kv = 133120). Per layer: set_rows of the 2048 new K and
+    V rows, causal flash attention over 133120 keys, sigmoid output gate.
+    Two forms: 'mask' = the engine's F16 mask + separate sigmoid_mul kernel;
+    'fused' = causal-from-positions + the gate fused into the epilogue."""
+    n_kv = STACK_START + STACK_N_Q
+    ks, vs = [], []
+    for li in range(N_LAYERS):  # caches filled in-place to keep peak memory low
+        k, v = fill_caches(sqa, torch, dev, 1, n_kv, seed=100 + li)
+        ks += k
+        vs += v
+    q = torch.randn((STACK_N_Q, H, D), device=dev, dtype=torch.float32)
+    gate = torch.randn((STACK_N_Q, H, D), device=dev, dtype=torch.float32)
+    knew = torch.randn((STACK_N_Q, HKV * D), device=dev, dtype=torch.float32)
+    vnew = torch.randn((STACK_N_Q, HKV * D), device=dev, dtype=torch.float32)
+    idx = torch.arange(STACK_START, n_kv, device=dev, dtype=torch.int64)
+    mask = torch.empty((STACK_N_Q, n_kv), dtype=torch.float16, device=dev)
+    sqa.fill_causal_mask(mask, STACK_START)
+    attn = torch.empty((STACK_N_Q, H, D), dtype=torch.float32, device=dev)
+    out = torch.empty((STACK_N_Q, H, D), dtype=torch.float32, device=dev)
+    ws = torch.empty(sqa.flash_attn_workspace_size(q, ks[0], n_kv), dtype=torch.uint8, device=dev)
+
+    def step_mask():
+        for li in range(N_LAYERS):
+            sqa.set_rows_q4_0(ks[li], knew, idx)
+            sqa.set_rows_q4_0(vs[li], vnew, idx)
+            sqa.flash_attn_ext(q, ks[li], vs[li], n_kv, mask=mask, out=attn, workspace=ws)
+            sqa.sigmoid_mul(attn.view(STACK_N_Q, H * D), gate.view(STACK_N_Q, H * D),
+                            out=out.view(STACK_N_Q, H * D))
+
+    def step_fused():
+        for li in range(N_LAYERS):
+            sqa.set_rows_q4_0(ks[li], knew, idx)
+            sqa.set_rows_q4_0(vs[li], vnew, idx)
+            sqa.flash_attn_ext_causal(q, ks[li], vs[li], n_kv, STACK_START, gate=gate, out=out, workspace=ws)
+
+    res = {"workload": f"{N_LAYERS}-layer stack: ubatch {STACK_N_Q} at prior context {STACK_START} "
+                       f"(n_kv={n_kv}), 16q/2kv, hd256, q4_0 K/V; set_rows -> FA -> sigmoid gate"}
+    flops = prefill_flops(STACK_N_Q, STACK_START)
+    for name, fn in (("mask", step_mask), ("fused", step_fused)):
+        for _ in range(warmup):
+            fn()
+        ms = time_steps(torch, fn, steps) / steps
+        sqa.profile_begin(steps * N_LAYERS * 8 + 16)
+        time_steps(torch, fn, steps)
+        sqa.profile_end()
+        kern = {}
+        for kn in ("set_rows_q4_0", "fa_prefill_prep", "fa_prefill", "fa_combine", "sigmoid_mul"):
+            t, c = sqa.profile_get(kn)
+            if c:
+                kern[kn] = round(t / c * 1e3, 2)
+        res[name] = {"ms_per_stack": round(ms, 3),
+                     "attn_TFLOP/s": round(N_LAYERS * flops / (ms * 1e-3) / 1e12, 1),
+                     "kernels_us": kern,
+                     "fa_prefill_frac_of_mfma_peak": round(flops / (kern["fa_prefill"] * 1e-6) / 1e12
+                                                           / MFMA_F16_PEAK_TFLOPS, 4)}
+    del ks, vs, mask, ws
+    return res
+
+
 def cpu_baseline(orc, kq, vq, q, mask, budget_s=8.0):
     """The oracle (C restatement of ggml's CPU flash_attn_ext) on this host."""
     threads = min(os.cpu_count() or 1, 16, q.shape[0] * q.shape[1])
@@ -91,6 +219,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-verify", action="store_true", help="skip the n_q=2 verify leg")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the pp512 prefill leg")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 10-layer ubatch-2048 stack leg")
+    ap.add_argument("--copy-ref", action="store_true",
+                    help="run a plain 256 MiB device copy at the end (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of this single-GPU path; --gpus {args.gpus} is not "
@@ -154,7 +286,7 @@ def main():
         "kernels_us": {"fa_decode": round(dec_avg_us, 2), "fa_combine": round(comb_avg_us, 2)},
         "roofline": {"kernel": "fa_decode", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": DECODE_TRAFFIC_BYTES,
                      "bytes_per_launch": layer_bytes(N_KV, 1)},
     }
 
@@ -177,6 +309,13 @@ def main():
                                 "GB/s": round(N_LAYERS * layer_bytes(N_KV, 2) / (ms2 * 1e-3) / 1e9, 1),
                                 "draft_row_marginal_pct": round(100 * (ms2 / ms_per_step - 1), 1)}
 
+    if not args.no_prefill:
+        result["prefill_pp512"] = prefill_leg(sqa, torch, dev, max(2, args.steps // 2), 2)
+        torch.cuda.empty_cache()
+    if not args.no_stack:
+        result["stack_ub2048_131k"] = stack_leg(sqa, torch, dev, 2, 1)
+        torch.cuda.empty_cache()
+
     if not args.no_cpu:
         from oracle import oracle as orc
 
@@ -194,6 +333,13 @@ def main():
         o_ref = orc.flash_attn_ext(qh, kq, vq, mh, threads=threads)
         rms = float(np.sqrt(np.mean(o_ref.astype(np.float64) ** 2)))
         result["parity_max_err_over_rms"] = float(np.abs(o_gpu - o_ref).max() / rms)
+
+    if args.copy_ref:
+        a = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
 
     print(json.dumps(result))
 

@@ -90,6 +90,8 @@ int check_fa(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
     const uint64_t dst_row = 4ull * kHeadDim;
     if (dst->nb[0] != 4 || dst->nb[1] != dst_row || dst->nb[2] != dst_row * (uint64_t)dst->ne[1])
         return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: dst must be contiguous");
+    if ((uintptr_t)dst->data % 16)
+        return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: dst data must be 16-byte aligned");
     const int64_t G = q->ne[2] / k->ne[2];
     *decode = q->ne[1] * G <= 16;
     if (*decode && k->ne[2] != 2)

@@ -594,14 +594,66 @@ __global__ __launch_bounds__(256) void fa_combine_kernel(const float *__restrict
     }
 }
 
+// The same merge for many rows and few splits (prefill): 64 threads per row,
+// one float4 of the row each, 4 rows per block; every thread walks the splits
+// itself (the (m, l) pairs are the same for the 64 threads of a row and come
+// from the cache).
+constexpr int kRowsMaxSplits = 32;
+__global__ __launch_bounds__(256) void fa_combine_rows_kernel(const float *__restrict__ part_acc,
+                                                              const float *__restrict__ part_ml,
+                                                              int n_splits, int rows_total,
+                                                              float *__restrict__ dst, const char *gate,
+                                                              int64_t gate_nb1, int64_t gate_nb2, int H) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int c = threadIdx.x & 63;
+    if (row >= rows_total) return;
+    float ms[kRowsMaxSplits];
+    float M = -INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < kRowsMaxSplits; ++sp) {
+        ms[sp] = sp < n_splits ? part_ml[((int64_t)sp * rows_total + row) * 2] : -INFINITY;
+        M = fmaxf(M, ms[sp]);
+    }
+    const int64_t sstride = (int64_t)rows_total * 256;
+    const float *pa = part_acc + (int64_t)row * 256 + 4 * c;
+    float L = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int sp = 0; sp < kRowsMaxSplits; ++sp) {
+        if (sp >= n_splits) break;
+        const float w = (M == -INFINITY || ms[sp] == -INFINITY) ? 0.0f : exp2f((ms[sp] - M) * kLog2e);
+        L = fmaf(part_ml[((int64_t)sp * rows_total + row) * 2 + 1], w, L);
+        const float4 a = *reinterpret_cast<const float4 *>(pa + sp * sstride);
+        o.x = fmaf(a.x, w, o.x);
+        o.y = fmaf(a.y, w, o.y);
+        o.z = fmaf(a.z, w, o.z);
+        o.w = fmaf(a.w, w, o.w);
+    }
+    const float inv = L == 0.0f ? 0.0f : 1.0f / L;
+    float r[4] = {o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+    if (gate) {
+        const int t = row / H, h = row % H;
+        const float *gp = reinterpret_cast<const float *>(gate + t * gate_nb2 + h * gate_nb1) + 4 * c;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[j] = r[j] * (1.0f / (1.0f + expf(-gp[j])));
+    }
+    *reinterpret_cast<float4 *>(dst + (int64_t)row * 256 + 4 * c) = make_float4(r[0], r[1], r[2], r[3]);
+}
+
 }  // namespace
 
 int launch_fa_combine(const float *part_acc, const float *part_ml, int n_splits, int rows_total,
                       float *dst, const sqa_tensor *gate, int H, hipStream_t s) {
+    const char *g = gate ? (const char *)gate->data : nullptr;
+    const int64_t g1 = gate ? (int64_t)gate->nb[1] : 0, g2 = gate ? (int64_t)gate->nb[2] : 0;
     const int prof = profile_start("fa_combine", s);
-    fa_combine_kernel<<<dim3((unsigned)rows_total, 16), dim3(256), 0, s>>>(
-        part_acc, part_ml, n_splits, rows_total, dst, gate ? (const char *)gate->data : nullptr,
-        gate ? (int64_t)gate->nb[1] : 0, gate ? (int64_t)gate->nb[2] : 0, H);
+    if (n_splits <= kRowsMaxSplits && rows_total >= 64) {
+        fa_combine_rows_kernel<<<dim3((unsigned)((rows_total + 3) / 4)), dim3(256), 0, s>>>(
+            part_acc, part_ml, n_splits, rows_total, dst, g, g1, g2, H);
+    } else {
+        fa_combine_kernel<<<dim3((unsigned)rows_total, 16), dim3(256), 0, s>>>(part_acc, part_ml, n_splits,
+                                                                            rows_total, dst, g, g1, g2, H);
+    }
     profile_stop(prof, s);
     return hip_status(hipGetLastError(), "fa_combine launch");
 }

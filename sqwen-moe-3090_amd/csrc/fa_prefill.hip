@@ -40,6 +40,14 @@ constexpr int kVRow = 64 + 16;    // LDS bytes per transposed V row (32 keys, pa
 constexpr int kMaxQ = 16 * kWaves;  // query positions per workgroup when G = 1
 constexpr float kLog2e = 1.4426950408889634f;
 
+// v if keep, else zeros; a per-component AND keeps the operand in registers
+// (a select between two uint4 objects can be lowered to a select of their
+// addresses, which forces both onto the scratch stack).
+__device__ __forceinline__ uint4 keep_if(uint4 v, bool keep) {
+    const uint32_t m = keep ? 0xffffffffu : 0u;
+    return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+}
+
 __device__ __forceinline__ float h2f(uint32_t bits) {
     const uint16_t b = (uint16_t)bits;
     _Float16 f;
@@ -262,6 +270,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
     int pre_nvalid = 0;
     const bool mask_loader = p.mask && tid < QB * 4;  // 4 lanes x 8 keys per query position
     const int mq = tid >> 2, mc = (tid & 3) * 8;
+    const bool mask_aligned = ((uintptr_t)p.mask % 16 == 0) && (p.mask_nb1 % 16 == 0);
     const uint16_t *kf_h = p.kf + (int64_t)kvh * p.n_kv * kHeadDim;
     const uint16_t *kfl_h = p.kfl + (int64_t)kvh * p.n_kv * kHeadDim;
     const uint16_t *vt_h = p.vt + (int64_t)kvh * kHeadDim * p.n_kv_pad;
@@ -283,25 +292,28 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             const int qq = q_base + (mask_loader ? mq : 0);
             const int64_t mrow = qq < p.n_q ? qq : 0;
             const uint16_t *mp = reinterpret_cast<const uint16_t *>(p.mask + mrow * p.mask_nb1) + kt;
-            uint16_t e[8];
+            if (mask_aligned && nvalid == kPK) {  // uniform; stays in flight
+                pmsk = *reinterpret_cast<const uint4 *>(mp + mc);
+            } else {  // last tile of a range or unaligned rows: waits here
+                uint16_t e[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) e[j] = mp[mc + j < nvalid ? mc + j : 0];
-            __builtin_memcpy(&pmsk, e, 16);
+                for (int j = 0; j < 8; ++j) e[j] = mp[mc + j < nvalid ? mc + j : 0];
+                __builtin_memcpy(&pmsk, e, 16);
+            }
         }
         pre_nvalid = nvalid;
     };
     auto store_tile = [&]() {
-        const uint4 z = make_uint4(0, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int c = tid + kThreads * i;
             const int key = c >> 5, col = c & 31;
             const bool ok = key < pre_nvalid;
-            *reinterpret_cast<uint4 *>(sK + key * kKRow + 16 * col) = ok ? pk[i] : z;
-            *reinterpret_cast<uint4 *>(sKl + key * kKRow + 16 * col) = ok ? pkl[i] : z;
+            *reinterpret_cast<uint4 *>(sK + key * kKRow + 16 * col) = keep_if(pk[i], ok);
+            *reinterpret_cast<uint4 *>(sKl + key * kKRow + 16 * col) = keep_if(pkl[i], ok);
             const int dim = c >> 2, seg = c & 3;
-            *reinterpret_cast<uint4 *>(sV + dim * kVRow + 16 * seg) = pv[i];
-            *reinterpret_cast<uint4 *>(sVl + dim * kVRow + 16 * seg) = pvl[i];
+            *reinterpret_cast<uint4 *>(sV + dim * kVRow + 16 * seg) = keep_if(pv[i], true);
+            *reinterpret_cast<uint4 *>(sVl + dim * kVRow + 16 * seg) = keep_if(pvl[i], true);
         }
         if (mask_loader) *reinterpret_cast<uint4 *>(sM + mq * kPK + mc) = pmsk;
     };
