@@ -1,0 +1,142 @@
+// fa_combine.hip - merges the split-KV partials of the decode and prefill
+// attention kernels: out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), with
+// M = max_s m_s (the log-sum-exp rule), optionally times sigmoid(gate) (the
+// output gate of src/model/attn.rs:282-283 in the reference). Partials:
+// acc [n_splits][rows][256] unnormalised, ml [n_splits][rows][2] = (m, l) with m
+// in natural-log units of the scaled logits.
+#include "common.hpp"
+
+namespace sqa {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Merge split partials: out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M),
+// optionally times sigmoid(gate). Grid: (rows, 16 chunks of 16 dims); 256
+// threads = 16 dims x 16 split groups, each thread summing every 16th split
+// with all its loads in flight; the split weights are computed once per block.
+constexpr int kMaxSplits = 1024;
+__global__ __launch_bounds__(256) void fa_combine_kernel(const float *__restrict__ part_acc,
+                                                         const float *__restrict__ part_ml,
+                                                         int n_splits, int rows_total,
+                                                         float *__restrict__ dst, const char *gate,
+                                                         int64_t gate_nb1, int64_t gate_nb2, int H) {
+    __shared__ float wts[kMaxSplits];
+    __shared__ float red[16][17];
+    __shared__ float redm[256];
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int dl = tid & 15;
+    const int sg = tid >> 4;
+    const int d = blockIdx.y * 16 + dl;
+    float mloc = -INFINITY;
+    for (int s = tid; s < n_splits; s += 256) mloc = fmaxf(mloc, part_ml[((int64_t)s * rows_total + row) * 2]);
+    redm[tid] = mloc;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) redm[tid] = fmaxf(redm[tid], redm[tid + w]);
+        __syncthreads();
+    }
+    const float M = redm[0];
+    __syncthreads();
+    float lloc = 0.0f;
+    for (int s = tid; s < n_splits; s += 256) {
+        const float ms = part_ml[((int64_t)s * rows_total + row) * 2];
+        const float ls = part_ml[((int64_t)s * rows_total + row) * 2 + 1];
+        const float w = (M == -INFINITY || ms == -INFINITY) ? 0.0f : exp2f((ms - M) * kLog2e);
+        wts[s] = w;
+        lloc += ls * w;
+    }
+    redm[tid] = lloc;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) redm[tid] += redm[tid + w];
+        __syncthreads();
+    }
+    const float L = redm[0];
+    const float *pa = part_acc + (int64_t)row * 256 + d;
+    const int64_t sstride = (int64_t)rows_total * 256;
+    float o = 0.0f;
+#pragma unroll 16
+    for (int s = sg; s < n_splits; s += 16) o = fmaf(pa[s * sstride], wts[s], o);
+    red[sg][dl] = o;
+    __syncthreads();
+    if (tid < 16) {
+        float ot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) ot += red[j][tid];
+        float r = (L == 0.0f) ? 0.0f : ot * (1.0f / L);
+        if (gate) {
+            const int t = row / H, h = row % H;
+            const float gv = reinterpret_cast<const float *>(gate + t * gate_nb2 + h * gate_nb1)[d];
+            r = r * (1.0f / (1.0f + expf(-gv)));
+        }
+        dst[(int64_t)row * 256 + d] = r;
+    }
+}
+
+// The same merge for many rows and few splits (prefill): 64 threads per row,
+// one float4 of the row each, 4 rows per block; every thread walks the splits
+// itself (the (m, l) pairs are the same for the 64 threads of a row and come
+// from the cache).
+constexpr int kRowsMaxSplits = 32;
+__global__ __launch_bounds__(256) void fa_combine_rows_kernel(const float *__restrict__ part_acc,
+                                                              const float *__restrict__ part_ml,
+                                                              int n_splits, int rows_total,
+                                                              float *__restrict__ dst, const char *gate,
+                                                              int64_t gate_nb1, int64_t gate_nb2, int H) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int c = threadIdx.x & 63;
+    if (row >= rows_total) return;
+    float ms[kRowsMaxSplits];
+    float M = -INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < kRowsMaxSplits; ++sp) {
+        ms[sp] = sp < n_splits ? part_ml[((int64_t)sp * rows_total + row) * 2] : -INFINITY;
+        M = fmaxf(M, ms[sp]);
+    }
+    const int64_t sstride = (int64_t)rows_total * 256;
+    const float *pa = part_acc + (int64_t)row * 256 + 4 * c;
+    float L = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int sp = 0; sp < kRowsMaxSplits; ++sp) {
+        if (sp >= n_splits) break;
+        const float w = (M == -INFINITY || ms[sp] == -INFINITY) ? 0.0f : exp2f((ms[sp] - M) * kLog2e);
+        L = fmaf(part_ml[((int64_t)sp * rows_total + row) * 2 + 1], w, L);
+        const float4 a = *reinterpret_cast<const float4 *>(pa + sp * sstride);
+        o.x = fmaf(a.x, w, o.x);
+        o.y = fmaf(a.y, w, o.y);
+        o.z = fmaf(a.z, w, o.z);
+        o.w = fmaf(a.w, w, o.w);
+    }
+    const float inv = L == 0.0f ? 0.0f : 1.0f / L;
+    float r[4] = {o.x * inv, o.y * inv, o.z * inv, o.w * inv};
+    if (gate) {
+        const int t = row / H, h = row % H;
+        const float *gp = reinterpret_cast<const float *>(gate + t * gate_nb2 + h * gate_nb1) + 4 * c;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[j] = r[j] * (1.0f / (1.0f + expf(-gp[j])));
+    }
+    *reinterpret_cast<float4 *>(dst + (int64_t)row * 256 + 4 * c) = make_float4(r[0], r[1], r[2], r[3]);
+}
+
+}  // namespace
+
+int launch_fa_combine(const float *part_acc, const float *part_ml, int n_splits, int rows_total,
+                      float *dst, const sqa_tensor *gate, int H, hipStream_t s) {
+    const char *g = gate ? (const char *)gate->data : nullptr;
+    const int64_t g1 = gate ? (int64_t)gate->nb[1] : 0, g2 = gate ? (int64_t)gate->nb[2] : 0;
+    const int prof = profile_start("fa_combine", s);
+    if (n_splits <= kRowsMaxSplits && rows_total >= 64) {
+        fa_combine_rows_kernel<<<dim3((unsigned)((rows_total + 3) / 4)), dim3(256), 0, s>>>(
+            part_acc, part_ml, n_splits, rows_total, dst, g, g1, g2, H);
+    } else {
+        fa_combine_kernel<<<dim3((unsigned)rows_total, 16), dim3(256), 0, s>>>(part_acc, part_ml, n_splits,
+                                                                            rows_total, dst, g, g1, g2, H);
+    }
+    profile_stop(prof, s);
+    return hip_status(hipGetLastError(), "fa_combine launch");
+}
+
+}  // namespace sqa
