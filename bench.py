@@ -260,9 +260,11 @@ def main():
     time_steps(torch, step, args.steps)
     sqa.profile_end()
     dec_ms, dec_n = sqa.profile_get("fa_decode")
-    comb_ms, comb_n = sqa.profile_get("fa_combine")
+    comb_ms, comb_n = sqa.profile_get("fa_combine")  # absent when the split merge is fused
     dec_avg_us = dec_ms / dec_n * 1e3
-    comb_avg_us = comb_ms / comb_n * 1e3
+    kernels = {"fa_decode": round(dec_avg_us, 2)}
+    if comb_n:
+        kernels["fa_combine"] = round(comb_ms / comb_n * 1e3, 2)
     achieved = layer_bytes(N_KV, 1) / (dec_avg_us * 1e-6) / 1e9
 
     result = {
@@ -283,7 +285,7 @@ def main():
                    "n_q": 1, "heads": H, "kv_heads": HKV, "head_dim": D},
         "per_layer_us": round(ms_per_step * 1e3 / N_LAYERS, 2),
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
-        "kernels_us": {"fa_decode": round(dec_avg_us, 2), "fa_combine": round(comb_avg_us, 2)},
+        "kernels_us": kernels,
         "roofline": {"kernel": "fa_decode", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": DECODE_TRAFFIC_BYTES,

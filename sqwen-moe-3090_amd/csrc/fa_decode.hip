@@ -498,7 +498,9 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
         sML[((kvh * 4 + wq) * 16 + n) * 2 + 1] = l_part;
     }
     __syncthreads();
-    // sAcc[kvh][wq][T][n][row]: float4 of rows 4g..4g+3 per (T, n)
+    // sAcc[kvh][wq][T][n][quad]: float4 of rows 4q..4q+3 per (T, n), the quad
+    // index XOR-swizzled with (n >> 1) & 3 so that 8 consecutive n of one quad
+    // hit 8 distinct bank groups (conflict-free 16-byte accesses).
     float *sAcc = reinterpret_cast<float *>(smem);
     if (4 * g < kRowsUsed) {
         float fac[4];
@@ -514,7 +516,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
 #pragma unroll
         for (int T = 0; T < 16; ++T) {
             const float4 o = make_float4(acc[T][0] * fac[0], acc[T][1] * fac[1], acc[T][2] * fac[2], acc[T][3] * fac[3]);
-            *reinterpret_cast<float4 *>(sAcc + ((((kvh * 4 + wq) * 16 + T) * 16 + n) * 16 + 4 * g)) = o;
+            *reinterpret_cast<float4 *>(sAcc + ((((kvh * 4 + wq) * 16 + T) * 16 + n) * 16 + 4 * (g ^ ((n >> 1) & 3)))) = o;
         }
     }
     __syncthreads();
@@ -529,7 +531,8 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
         float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int w2 = 0; w2 < 4; ++w2) {
-            const float4 v4 = *reinterpret_cast<const float4 *>(sAcc + ((((kh * 4 + w2) * 16 + T) * 16 + nn) * 16 + 4 * rq));
+            const float4 v4 = *reinterpret_cast<const float4 *>(
+                sAcc + ((((kh * 4 + w2) * 16 + T) * 16 + nn) * 16 + 4 * (rq ^ ((nn >> 1) & 3))));
             sum.x += v4.x;
             sum.y += v4.y;
             sum.z += v4.z;
