@@ -209,6 +209,7 @@ struct PrefillParams {
     int64_t q_pos0;    // >= 0: causal from positions
     float scale;
     int n_splits;
+    int q_tiles;        // workgroups per (KV head, split)
     int64_t split_len;  // keys per split, a multiple of kPK
     float *part_acc, *part_ml;  // n_splits > 1
     float *dst;                 // n_splits == 1: [n_q][H][256]
@@ -225,10 +226,19 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
     uint16_t *sM = reinterpret_cast<uint16_t *>(sVl + kHeadDim * kVRow);  // [queries][32]
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
-    const int kvh = blockIdx.y, split = blockIdx.z;
+    // Workgroups are dealt round-robin to the 8 XCDs (each with its own L2).
+    // Renumber so that each XCD gets a contiguous run of ids, i.e. the query
+    // tiles of the same (KV head, split): they stream the same K/V range, which
+    // that XCD's L2 then serves to all of them.
+    const int nb = (int)gridDim.x;
+    const int lin = (int)blockIdx.x;
+    const int id = nb % 8 == 0 ? (lin % 8) * (nb / 8) + lin / 8 : lin;
+    const int q_tile = id % p.q_tiles;
+    const int grp = id / p.q_tiles;
+    const int kvh = grp / p.n_splits, split = grp % p.n_splits;
     const int QW = 16 / p.G;           // query positions per wave
     const int QB = QW * kWaves;        // query positions per workgroup
-    const int q_base = blockIdx.x * QB;
+    const int q_base = q_tile * QB;
 
     // This lane's query row (column n of S^T and row n of the P*V A operand).
     const int my_q = q_base + wave * QW + n / p.G;
@@ -559,6 +569,7 @@ int launch_fa_prefill(const FaArgs &a, hipStream_t s) {
     p.q_pos0 = a.q_pos0;
     p.scale = a.scale;
     p.n_splits = pl.n_splits;
+    p.q_tiles = pl.q_tiles;
     p.split_len = pl.split_len;
     p.part_acc = reinterpret_cast<float *>(base + pl.off_pa);
     p.part_ml = reinterpret_cast<float *>(base + pl.off_pm);
@@ -575,8 +586,7 @@ int launch_fa_prefill(const FaArgs &a, hipStream_t s) {
         lds_ok = true;
     }
     prof = profile_start("fa_prefill", s);
-    fa_prefill_kernel<<<dim3((unsigned)pl.q_tiles, (unsigned)Hkv, (unsigned)pl.n_splits), dim3(kThreads), kLdsBytes,
-                        s>>>(p);
+    fa_prefill_kernel<<<dim3((unsigned)(pl.q_tiles * Hkv * pl.n_splits)), dim3(kThreads), kLdsBytes, s>>>(p);
     profile_stop(prof, s);
     e = hipGetLastError();
     if (e != hipSuccess) return hip_status(e, "fa_prefill launch");
