@@ -30,8 +30,16 @@ def sources():
     return sorted(glob.glob(os.path.join(csrc, "*.hip")) + glob.glob(os.path.join(csrc, "*.cpp")))
 
 
+# Per-source extra flags. fa_prefill.hip: its MFMA accumulators are read and
+# rescaled by VALU code, so keep every MFMA result in VGPRs (the AGPR form makes
+# the register allocator copy the 128-register accumulator on every tile).
+EXTRA_FLAGS = {
+    "fa_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+}
+
+
 def _compile(src, out):
-    cmd = [HIPCC] + CFLAGS + ["-c", src, "-o", out]
+    cmd = [HIPCC] + CFLAGS + EXTRA_FLAGS.get(os.path.basename(src), []) + ["-c", src, "-o", out]
     r = subprocess.run(cmd, capture_output=True, text=True)
     errs = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:

@@ -1,26 +1,51 @@
-// fa_prefill.hip - FlashAttention for prefill chunks (n_q * H/Hkv > 16 query
-// rows per KV head): the ubatch node of src/model/attn.rs:228-251 in the
-// reference (n_q = 512 or 2048 over a q4_0 cache of 16K-133K keys).
+// fa_prefill.hip - FlashAttention for prefill chunks (more than 16 query rows
+// per KV head, or more than 4 positions): the ubatch node of
+// src/model/attn.rs:228-251 in the reference (n_q = 512 or 2048 over a q4_0
+// cache of 16K-133K keys).
 //
 // Three short pre-passes, then one MFMA kernel:
-//   kdeq  K q4_0 -> Kf  fp16 hi, lo [Hkv][n_kv][256]
-//   vdeq  V q4_0 -> Vt  fp16 hi, lo [Hkv][256][n_kv_pad]  (transposed: keys contiguous)
-//   qprep Q f32  -> q8_0 (ggml's x86 rounding) -> Q' = q8*d
-// Every dequantized value x = (nib-8)*d or q8*d is split as hi = fp16(x),
-// lo = fp16(x - hi); x needs at most 18 significant bits and hi + lo hold 22,
-// so Q', K and V enter the MFMAs exactly. Only P is rounded to fp16 once.
-// K/V are dequantized once per call instead of once per query tile.
+//   kdeq  K q4_0 -> per 32-key tile: Kh, Kl fp16 [32 keys][256] with
+//                 x = (nib-8)*d = Kh + Kl exactly (x has <= 14 significant
+//                 bits, Kh + Kl hold 22)
+//   vdeq  V q4_0 -> per tile: Vc fp16 codes [256 dims][32 keys] and Dv fp16
+//                 scales [8 blocks][32 keys]; per KV head the largest |d_v|
+//   qprep Q f32  -> q8_0 with ggml's x86 rounding (d = amax/127, codes =
+//                 rint(x * 127/amax)): codes as fp16 integers [n_q*H][256] and
+//                 fp16(d) * scale * log2(e) as f32 [n_q*H][8]
+// A tile of one KV head is a contiguous 49664-byte record [Kh | Kl | Vc | Dv]
+// laid out exactly as the main kernel wants it in LDS (rows permuted, chunks
+// swizzled, see below), so its K and V halves move HBM -> LDS as straight
+// copies. Keys past n_kv are zero.
 //
-// fa_prefill_kernel: a workgroup takes 16 query rows per wave x 8 waves of
-// ONE KV head (GQA packing: with 8 q heads per KV head that is 16 positions x
-// 8 heads), streams 32-key tiles of Kf and Vt through LDS and runs
-//   S^T = K Q'^T  on v_mfma_f32_16x16x32_f16: Kh.Qh + Kh.Ql + Kl.Qh (the
-//                 Kl.Ql term is below 2^-22 relative and dropped),
-//   online softmax in fp32,
-//   O  += P V     on v_mfma_f32_16x16x32_f16: P.Vh + P.Vl (P rounded to fp16).
-// Computing S^T (keys as rows) leaves each lane with 8 logits of one query
-// row, which is exactly the A-operand layout of the P*V MFMA. Long key ranges
-// with few query tiles are split across workgroups and merged by fa_combine.
+// fa_prefill_kernel: a workgroup takes 128 query rows of ONE KV head (GQA
+// packed: row r is position r / G, head kvh*G + r % G) and streams 32-key
+// tiles. Its 8 wavefronts (2 per SIMD) split the work by kind:
+//   score wave w (0..3), rows 32w..32w+31, holds their Q codes (64 registers):
+//     S^T = sum over q4_0 blocks b of d_q[b] * (Kh_b.q_b + Kl_b.q_b), the
+//     products on v_mfma_f32_16x16x32_f16 (all exact in fp32) and the d_q
+//     scaling (with scale * log2 e) as an fp32 FMA; then the mask and the
+//     online softmax in fp32 (base 2, rescaled whenever a row maximum grows, so
+//     the largest P is exactly 1). P (fp32) and the rescale factors go to LDS.
+//   value wave 4 + w, the same 32 rows, holds their O (128 registers) one tile
+//     behind: O = alpha O + P V per block b with
+//     A = fp16(P 2^e d_v) (one rounding, the only one on the path) and B = the
+//     exact V codes. 2^e is one power of two per KV head that brings max |d_v|
+//     into [1, 2): it keeps A clear of fp16 subnormals and overflow, and
+//     cancels in O = PV / l because l is summed from the same scaled P.
+// Computing S^T (keys as rows) leaves each lane with 8 logits of one query row
+// in the A-operand layout of the P*V MFMA. K rows sit in LDS in the order
+// r -> key sigma(r) = 8*((r>>2)&3) + 4*(r>>4) + (r&3), which makes a lane's 8
+// logits keys 8g..8g+7, so its V operand is one 16-byte run of a Vc row.
+//
+// LDS reads are ds_read_b64 (16 lanes a pass). To keep them conflict free,
+// 16-byte chunk c of K row r is stored at chunk c ^ (r & 7) with its 8-byte
+// halves swapped when r & 8, and chunk c of Vc row d at c ^ ((d >> 1) & 3),
+// halves swapped when d & 8.
+//
+// Tiles move HBM -> LDS with global_load_lds_dwordx4: in iteration t the K half
+// (and mask rows) of tile t + 1 and the V half of tile t are in flight while
+// the score waves work on tile t and the value waves on tile t - 1; one
+// barrier per iteration.
 //
 // Operand layout of the 16x16x32 MFMAs (64 lanes, lane = 16*g + n):
 //   A: A[row n][k = 8g..8g+7]   B: B[k = 8g..8g+7][col n]   C: C[rows 4g..4g+3][col n]
@@ -32,21 +57,32 @@ namespace {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
-constexpr int kPK = 32;           // keys per tile
-constexpr int kWaves = 8;         // 16 query rows each
+constexpr int kPK = 32;                  // keys per tile
+constexpr int kScoreWaves = 4;           // 32 rows each
+constexpr int kValueWaves = 4;           // 32 rows each
+constexpr int kWaves = kScoreWaves + kValueWaves;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kKRow = 512 + 16;   // LDS bytes per fp16 K row (padded against bank conflicts)
-constexpr int kVRow = 64 + 16;    // LDS bytes per transposed V row (32 keys, padded)
-constexpr int kMaxQ = 16 * kWaves;  // query positions per workgroup when G = 1
+constexpr int kRG = 2;                   // 16-row groups per score wave
+constexpr int kRowsPerWG = kScoreWaves * kRG * 16;  // 128 query rows
+constexpr int kOffKl = kPK * 512;        // inside the K half: Kl after Kh
+constexpr int kKHalf = 2 * kOffKl;       // Kh + Kl: 32768 bytes
+constexpr int kOffDv = kHeadDim * kPK * 2;  // inside the V half: Dv after Vc
+constexpr int kVHalf = kOffDv + 8 * kPK * 2;  // Vc + Dv: 16896 bytes
+constexpr int kTileBytes = kKHalf + kVHalf;   // one tile record
+constexpr int kKInst = kKHalf / 1024;    // 32 DMA instructions
+constexpr int kVInst = (kVHalf + 1023) / 1024;  // 17, the last one 512 bytes
+constexpr int kKStage = kKHalf, kVStage = kVInst * 1024;
+// LDS map: 2 K stages | 2 V stages | 2 P buffers | 2 rescale buffers | 2 mask stages
+constexpr int kLdsV = 2 * kKStage;
+constexpr int kLdsP = kLdsV + 2 * kVStage;        // [4 waves][2 rg][2 halves][64 lanes][16 B]
+constexpr int kPBuf = kScoreWaves * kRG * 2 * 1024;
+constexpr int kLdsA = kLdsP + 2 * kPBuf;          // [4 waves][2 rg][16 rows] f32
+constexpr int kABuf = kScoreWaves * kRG * 16 * 4;
+constexpr int kLdsMask = kLdsA + 2 * kABuf;       // [qb positions][32 keys] f16
 constexpr float kLog2e = 1.4426950408889634f;
 
-// v if keep, else zeros; a per-component AND keeps the operand in registers
-// (a select between two uint4 objects can be lowered to a select of their
-// addresses, which forces both onto the scratch stack).
-__device__ __forceinline__ uint4 keep_if(uint4 v, bool keep) {
-    const uint32_t m = keep ? 0xffffffffu : 0u;
-    return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
-}
+static_assert(kTileBytes == 49664 && kTileBytes % 256 == 0, "tile record");
+static_assert(kLdsMask + 2 * 128 * kPK * 2 <= 160 * 1024, "LDS budget");
 
 __device__ __forceinline__ float h2f(uint32_t bits) {
     const uint16_t b = (uint16_t)bits;
@@ -54,6 +90,13 @@ __device__ __forceinline__ float h2f(uint32_t bits) {
     __builtin_memcpy(&f, &b, 2);
     return (float)f;
 }
+
+__device__ __forceinline__ uint4 swap_halves(uint4 v, bool swap) {
+    return swap ? make_uint4(v.z, v.w, v.x, v.y) : v;
+}
+
+// LDS/record row of key k (0..31) of a tile: the inverse of sigma.
+__device__ __forceinline__ int key_row(int k) { return 16 * ((k >> 2) & 1) + 4 * (k >> 3) + (k & 3); }
 
 // ---------------------------------------------------------------- pre-passes
 
@@ -65,19 +108,22 @@ __device__ __forceinline__ void split_hl(float x, uint16_t &hi, uint16_t &lo) {
     __builtin_memcpy(&lo, &l, 2);
 }
 
-// One thread per q4_0 block of K: 18 bytes in, 32 fp16 hi + 32 fp16 lo out.
+// One thread per q4_0 block of K (zeros for keys past n_kv): 18 bytes in,
+// 32 fp16 Kh + 32 fp16 Kl out, as 4 + 4 swizzled 16-byte chunks of the key's row.
+// Thread 0 also clears the per-head |d_v| maxima that vdeq accumulates.
 __global__ __launch_bounds__(256) void kdeq_kernel(const uint8_t *__restrict__ k, int64_t nb1, int64_t nb2,
-                                                   int64_t n_kv, int hkv, uint16_t *__restrict__ kf,
-                                                   uint16_t *__restrict__ kfl) {
+                                                   int64_t n_kv, int64_t kv_tiles, int hkv,
+                                                   uint8_t *__restrict__ kv, uint32_t *__restrict__ dvmax) {
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t total = n_kv * hkv * kBlocksPerHead;
-    if (gid >= total) return;
+    if (gid < hkv) dvmax[gid] = 0;
+    if (gid >= kv_tiles * kPK * hkv * kBlocksPerHead) return;
     const int b = (int)(gid % kBlocksPerHead);
     const int64_t kh = gid / kBlocksPerHead;  // key * hkv + head
     const int h = (int)(kh % hkv);
     const int64_t key = kh / hkv;
-    const uint16_t *src = reinterpret_cast<const uint16_t *>(k + key * nb1 + h * nb2 + 18 * b);
-    const float d = h2f(src[0]);
+    const bool ok = key < n_kv;
+    const uint16_t *src = reinterpret_cast<const uint16_t *>(k + (ok ? key : 0) * nb1 + h * nb2 + 18 * b);
+    const float d = ok ? h2f(src[0]) : 0.0f;
     uint16_t out[32], outl[32];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -88,78 +134,88 @@ __global__ __launch_bounds__(256) void kdeq_kernel(const uint8_t *__restrict__ k
         split_hl((float)((b0 >> 4) - 8) * d, out[16 + 2 * j], outl[16 + 2 * j]);
         split_hl((float)((b1 >> 4) - 8) * d, out[16 + 2 * j + 1], outl[16 + 2 * j + 1]);
     }
-    const int64_t off = ((int64_t)h * n_kv + key) * kHeadDim + 32 * b;
-    uint4 *dst = reinterpret_cast<uint4 *>(kf + off);
-    uint4 *dstl = reinterpret_cast<uint4 *>(kfl + off);
+    const int r = key_row((int)(key & (kPK - 1)));
+    uint8_t *row = kv + ((int64_t)h * kv_tiles + (key >> 5)) * kTileBytes + r * 512;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+        const int pos = (4 * b + j) ^ (r & 7);
         uint4 v, w;
         __builtin_memcpy(&v, out + 8 * j, 16);
         __builtin_memcpy(&w, outl + 8 * j, 16);
-        dst[j] = v;
-        dstl[j] = w;
+        *reinterpret_cast<uint4 *>(row + 16 * pos) = swap_halves(v, r & 8);
+        *reinterpret_cast<uint4 *>(row + kOffKl + 16 * pos) = swap_halves(w, r & 8);
     }
 }
 
-// One workgroup per (64 keys, head): thread t handles keys 8*(t%8)..+7 of the
-// 8 dims {32beta + 4w + j, 32beta + 16 + 4w + j} (beta = t/32, w = (t/8)%4), and
-// writes each dim's 8 keys as one 16-byte row segment of Vt. Keys past n_kv
-// are written as zeros, so the padded tail of Vt is finite.
+// One workgroup per (64 keys, head): thread t handles keys 8*(t%8)..+7 (one
+// 16-byte chunk of a Vc row) of the 8 dims {32beta + 4w + j, 32beta + 16 + 4w + j}
+// (beta = t/32, w = (t/8)%4); threads with w == 0 also write the 8 keys' d_v of
+// block beta. Keys past n_kv get zero codes and scales. Each wavefront folds
+// the largest |d_v| it saw into dvmax[head] (fp16 magnitude bits).
 __global__ __launch_bounds__(256) void vdeq_kernel(const uint8_t *__restrict__ v, int64_t nb1, int64_t nb2,
-                                                   int64_t n_kv, int64_t n_kv_pad, uint16_t *__restrict__ vt,
-                                                   uint16_t *__restrict__ vtl) {
+                                                   int64_t n_kv, int64_t kv_tiles, uint8_t *__restrict__ kv,
+                                                   uint32_t *__restrict__ dvmax) {
     const int t = threadIdx.x;
     const int h = blockIdx.y;
     const int64_t k0 = (int64_t)blockIdx.x * 64 + 8 * (t & 7);
     const int beta = t >> 5;
     const int w = (t >> 3) & 3;
-    uint16_t lo[8][4], hi[8][4], lol[8][4], hil[8][4];  // [key][j], hi/lo parts
+    uint16_t lo[8][4], hi[8][4], dd[8];  // [key][j]
+    uint32_t dmax = 0;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
         const int64_t key = k0 + kk;
         const bool ok = key < n_kv;
         const uint16_t *blk = reinterpret_cast<const uint16_t *>(v + (ok ? key : 0) * nb1 + h * nb2 + 18 * beta);
-        const float d = ok ? h2f(blk[0]) : 0.0f;
+        dd[kk] = ok ? blk[0] : 0;
+        const uint32_t mag = dd[kk] & 0x7fffu;
+        dmax = mag > dmax ? mag : dmax;
         const uint32_t q01 = blk[1 + 2 * w], q23 = blk[2 + 2 * w];
-        const uint32_t x = q01 | (q23 << 16);  // qs[4w..4w+3]
+        const uint32_t x = ok ? (q01 | (q23 << 16)) : 0x88888888u;  // qs[4w..4w+3]; code 8 -> 0
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int byte = (x >> (8 * j)) & 0xff;
-            split_hl((float)((byte & 15) - 8) * d, lo[kk][j], lol[kk][j]);
-            split_hl((float)((byte >> 4) - 8) * d, hi[kk][j], hil[kk][j]);
+            const _Float16 l = (_Float16)((byte & 15) - 8), u = (_Float16)((byte >> 4) - 8);
+            __builtin_memcpy(&lo[kk][j], &l, 2);
+            __builtin_memcpy(&hi[kk][j], &u, 2);
         }
     }
+    uint8_t *vrec = kv + ((int64_t)h * kv_tiles + (k0 >> 5)) * kTileBytes + kKHalf;
+    const int c = (int)((k0 & (kPK - 1)) >> 3);  // chunk of the Vc row
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        uint16_t row_lo[8], row_hi[8], row_lol[8], row_hil[8];
+        uint16_t row_lo[8], row_hi[8];
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
             row_lo[kk] = lo[kk][j];
             row_hi[kk] = hi[kk][j];
-            row_lol[kk] = lol[kk][j];
-            row_hil[kk] = hil[kk][j];
         }
-        const int dlo = 32 * beta + 4 * w + j;
-        uint4 a, b, c, e;
+        const int dlo = 32 * beta + 4 * w + j, dhi = dlo + 16;
+        uint4 a, b;
         __builtin_memcpy(&a, row_lo, 16);
         __builtin_memcpy(&b, row_hi, 16);
-        __builtin_memcpy(&c, row_lol, 16);
-        __builtin_memcpy(&e, row_hil, 16);
-        const int64_t o0 = ((int64_t)h * kHeadDim + dlo) * n_kv_pad + k0;
-        const int64_t o1 = ((int64_t)h * kHeadDim + dlo + 16) * n_kv_pad + k0;
-        *reinterpret_cast<uint4 *>(vt + o0) = a;
-        *reinterpret_cast<uint4 *>(vt + o1) = b;
-        *reinterpret_cast<uint4 *>(vtl + o0) = c;
-        *reinterpret_cast<uint4 *>(vtl + o1) = e;
+        *reinterpret_cast<uint4 *>(vrec + 64 * dlo + 16 * (c ^ ((dlo >> 1) & 3))) = swap_halves(a, dlo & 8);
+        *reinterpret_cast<uint4 *>(vrec + 64 * dhi + 16 * (c ^ ((dhi >> 1) & 3))) = swap_halves(b, dhi & 8);
     }
+    if (w == 0) {
+        uint4 a;
+        __builtin_memcpy(&a, dd, 16);
+        *reinterpret_cast<uint4 *>(vrec + kOffDv + 64 * beta + 16 * c) = a;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint32_t other = (uint32_t)__shfl_xor((int)dmax, o);
+        dmax = other > dmax ? other : dmax;
+    }
+    if ((t & 63) == 0) atomicMax(dvmax + h, dmax);
 }
 
 // One thread per 32-value block of one (query, head) row: q8_0 with ggml's x86
-// rounding (d = amax/127, codes = rint(x * 127/amax)), then Q' = code * fp16(d)
-// (exact in fp32) split as hi = fp16(Q'), lo = fp16(Q' - hi) (exact).
+// rounding (d = amax/127, codes = rint(x * 127/amax)); the codes as fp16
+// (exact integers) and fp16(d) * scale * log2(e) as f32.
 __global__ __launch_bounds__(256) void qprep_kernel(const char *__restrict__ q, int64_t nb1, int64_t nb2,
-                                                    int n_q, int H, uint16_t *__restrict__ qhi,
-                                                    uint16_t *__restrict__ qlo) {
+                                                    int n_q, int H, float qscale, uint16_t *__restrict__ qc,
+                                                    float *__restrict__ qd) {
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (gid >= (int64_t)n_q * H * kBlocksPerHead) return;
     const int b = (int)(gid % kBlocksPerHead);
@@ -176,41 +232,72 @@ __global__ __launch_bounds__(256) void qprep_kernel(const char *__restrict__ q, 
     }
     const float d = amax / 127.f;
     const float id = amax != 0.0f ? 127.f / amax : 0.0f;
-    const float dh = (float)(_Float16)d;
-    uint16_t oh[32], ol[32];
+    uint16_t oc[32];
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
-        const float qq = rintf(v[j] * id) * dh;  // exact: 7-bit code x 11-bit scale
-        const _Float16 hh = (_Float16)qq;
-        const _Float16 ll = (_Float16)(qq - (float)hh);
-        __builtin_memcpy(&oh[j], &hh, 2);
-        __builtin_memcpy(&ol[j], &ll, 2);
+        const _Float16 cv = (_Float16)rintf(v[j] * id);
+        __builtin_memcpy(&oc[j], &cv, 2);
     }
-    uint4 *dh4 = reinterpret_cast<uint4 *>(qhi + row * kHeadDim + 32 * b);
-    uint4 *dl4 = reinterpret_cast<uint4 *>(qlo + row * kHeadDim + 32 * b);
+    uint4 *dc4 = reinterpret_cast<uint4 *>(qc + row * kHeadDim + 32 * b);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        uint4 a, c;
-        __builtin_memcpy(&a, oh + 8 * j, 16);
-        __builtin_memcpy(&c, ol + 8 * j, 16);
-        dh4[j] = a;
-        dl4[j] = c;
+        uint4 a;
+        __builtin_memcpy(&a, oc + 8 * j, 16);
+        dc4[j] = a;
+    }
+    qd[row * kBlocksPerHead + b] = (float)(_Float16)d * qscale;
+}
+
+// Copies an F16 mask whose rows are unaligned or whose length is not a
+// multiple of 8 into [n_q][len8] rows (len8 = n_kv rounded up to 8, -inf pad).
+__global__ __launch_bounds__(256) void pf_mask_pack_kernel(const char *__restrict__ src, int64_t nb1, int64_t n_kv,
+                                                           int n_q, int64_t len8, uint16_t *__restrict__ dst) {
+    const int64_t total = len8 * n_q;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int64_t t = i / len8, kk = i - t * len8;
+        dst[i] = kk < n_kv ? reinterpret_cast<const uint16_t *>(src + t * nb1)[kk] : (uint16_t)0xFC00;
     }
 }
 
 // ------------------------------------------------------------ main kernel
 
+// 16 bytes per lane from sbase + voff into LDS at m0 + 16 * lane (asynchronous;
+// the caller waits with s_waitcnt vmcnt).
+__device__ __forceinline__ void dma16(uint32_t voff, const void *sbase, uint32_t m0v) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0v)
+                 : "memory");
+}
+
+// Two 8-byte LDS reads into one MFMA operand. volatile keeps them two single
+// ds_read_b64 straight into the operand's registers: merged into ds_read2 pairs
+// they would bring halves of different operands and need register moves.
+__device__ __forceinline__ half8 lds_half8(const uint8_t *base, int off_lo, int off_hi) {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    typedef const volatile __attribute__((address_space(3))) u32x2 lds_u32x2;
+    const u32x2 a = *(lds_u32x2 *)(base + off_lo);
+    const u32x2 b = *(lds_u32x2 *)(base + off_hi);
+    const uint4 u = make_uint4(a.x, a.y, b.x, b.y);
+    half8 h;
+    __builtin_memcpy(&h, &u, 16);
+    return h;
+}
+
+
 struct PrefillParams {
-    const uint16_t *kf, *kfl, *vt, *vtl, *qhi, *qlo;
-    int64_t n_kv, n_kv_pad;
+    const uint8_t *kv;        // [Hkv][kv_tiles] tile records
+    const uint32_t *dvmax;    // [Hkv] fp16 magnitude bits
+    const uint16_t *qc;       // [n_q*H][256] fp16 codes
+    const float *qd;          // [n_q*H][8]
+    int64_t n_kv, kv_tiles;
     int n_q, H, G, Hkv;
-    const char *mask;  // F16 [n_kv, >= n_q] or null
-    int64_t mask_nb1;
-    int64_t q_pos0;    // >= 0: causal from positions
-    float scale;
+    const char *mask;  // F16 rows 16-byte aligned, mask_len (a multiple of 8) keys each, or null
+    int64_t mask_nb1, mask_len;
+    int64_t q_pos0;    // >= 0: causal from positions (mask ignored)
     int n_splits;
     int q_tiles;        // workgroups per (KV head, split)
     int64_t split_len;  // keys per split, a multiple of kPK
+    int qb;             // query positions per workgroup (128 / G)
+    int mask_stage;     // LDS bytes per mask stage (qb x 64)
     float *part_acc, *part_ml;  // n_splits > 1
     float *dst;                 // n_splits == 1: [n_q][H][256]
     const char *gate;
@@ -219,13 +306,11 @@ struct PrefillParams {
 
 __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
-    uint8_t *sK = smem;                          // hi: [32 keys][kKRow]
-    uint8_t *sKl = smem + kPK * kKRow;           // lo
-    uint8_t *sV = smem + 2 * kPK * kKRow;        // hi: [256 dims][kVRow]
-    uint8_t *sVl = sV + kHeadDim * kVRow;        // lo
-    uint16_t *sM = reinterpret_cast<uint16_t *>(sVl + kHeadDim * kVRow);  // [queries][32]
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
     // Workgroups are dealt round-robin to the 8 XCDs (each with its own L2).
     // Renumber so that each XCD gets a contiguous run of ids, i.e. the query
     // tiles of the same (KV head, split): they stream the same K/V range, which
@@ -236,272 +321,364 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
     const int q_tile = id % p.q_tiles;
     const int grp = id / p.q_tiles;
     const int kvh = grp / p.n_splits, split = grp % p.n_splits;
-    const int QW = 16 / p.G;           // query positions per wave
-    const int QB = QW * kWaves;        // query positions per workgroup
-    const int q_base = q_tile * QB;
-
-    // This lane's query row (column n of S^T and row n of the P*V A operand).
-    const int my_q = q_base + wave * QW + n / p.G;
-    const int my_h = kvh * p.G + n % p.G;
-    const bool row_ok = my_q < p.n_q;
-    const int my_ql = wave * QW + n / p.G;  // query index inside the workgroup
+    const int q_base = q_tile * p.qb;
 
     // Key range: the split, cut at the last key any query of the workgroup sees.
-    int64_t k_begin = (int64_t)split * p.split_len;
+    const int64_t k_begin = (int64_t)split * p.split_len;
     int64_t k_end = k_begin + p.split_len < p.n_kv ? k_begin + p.split_len : p.n_kv;
     if (p.q_pos0 >= 0) {
-        const int64_t q_last = (q_base + QB < p.n_q ? q_base + QB : p.n_q) - 1;
+        const int64_t q_last = (q_base + p.qb < p.n_q ? q_base + p.qb : p.n_q) - 1;
         const int64_t lim = p.q_pos0 + q_last + 1;
         if (k_end > lim) k_end = lim;
     }
+    const int n_tiles = k_end > k_begin ? (int)((k_end - k_begin + kPK - 1) / kPK) : 0;
 
-    // Q' (hi, lo) as B operands: lane holds row n, dims 32ks + 8g .. +7.
-    half8 bqh[8], bql[8];
+    // ---------------- DMA: 1 KB per instruction, a fixed share per wave ---------
+    // Iteration t: K half + mask of tile t + 1, V half of tile t (stage = tile & 1).
+    // K instruction jj (0..31) goes to wave jj % 8, V instruction jj (0..16, the
+    // last one 512 bytes) to wave (jj + 4) % 8, mask instruction jm (< 8) to wave
+    // (jm + 2) % 8.
+    const int n_mask_inst = p.mask ? (p.qb + 15) / 16 : 0;
+    const uint8_t *kv_h = p.kv + (int64_t)kvh * p.kv_tiles * kTileBytes;
+    const int jk0 = wave, jv0 = (wave + 4) % kWaves, jm = (wave + kWaves - 2) % kWaves;
+    const bool has_m = jm < n_mask_inst;
+    // mask row of this lane's slot in instruction jm: position q_base + r (clamped
+    // to n_q - 1), chunk c = (s & 3) ^ ((r >> 1) & 3) of the row's 32 keys
+    const int m_r = (64 * jm + lane) >> 2;
+    const int m_c = ((64 * jm + lane) & 3) ^ ((m_r >> 1) & 3);
+    const uint32_t m_row =
+        has_m ? (uint32_t)((int64_t)(q_base + m_r < p.n_q ? q_base + m_r : p.n_q - 1) * p.mask_nb1) : 0u;
+    const bool m_lane = m_r < p.qb;
+    auto issue = [&](int t_k, int t_v) {  // tile indices or -1
+        if (t_k >= 0) {
+            const int64_t kt = k_begin + (int64_t)t_k * kPK;
+            const uint8_t *rec = kv_h + (kt / kPK) * kTileBytes;
+            const uint32_t st = lds0 + (uint32_t)((t_k & 1) * kKStage);
+#pragma unroll
+            for (int i = 0; i < kKInst / kWaves; ++i) {
+                const int jj = jk0 + kWaves * i;
+                dma16(1024u * jj + 16u * lane, rec, st + 1024u * jj);
+            }
+            if (has_m) {
+                const int64_t col = kt + 8 * m_c < p.mask_len ? kt + 8 * m_c : p.mask_len - 8;
+                const uint32_t sm = lds0 + (uint32_t)(kLdsMask + (t_k & 1) * p.mask_stage + 1024 * jm);
+                if (m_lane) dma16(m_row + (uint32_t)(2 * col), p.mask, sm);
+            }
+        }
+        if (t_v >= 0) {
+            const int64_t kt = k_begin + (int64_t)t_v * kPK;
+            const uint8_t *rec = kv_h + (kt / kPK) * kTileBytes + kKHalf;
+            const uint32_t st = lds0 + (uint32_t)(kLdsV + (t_v & 1) * kVStage);
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const int jj = jv0 + kWaves * i;
+                if (jj < kVInst - 1 || (jj == kVInst - 1 && lane < 32))
+                    dma16(1024u * jj + 16u * lane, rec, st + 1024u * jj);
+            }
+        }
+    };
+    if (n_tiles > 0) issue(0, -1);
+
+    // e with max |d_v| * 2^e in [1, 2); P carries 2^e (added to the exponent)
+    float eshift = 0.0f;
     {
-        const int64_t roff = ((int64_t)(row_ok ? my_q : 0) * p.H + my_h) * kHeadDim;
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            const uint4 a = *reinterpret_cast<const uint4 *>(p.qhi + roff + 32 * ks + 8 * g);
-            const uint4 b = *reinterpret_cast<const uint4 *>(p.qlo + roff + 32 * ks + 8 * g);
-            __builtin_memcpy(&bqh[ks], &a, 16);
-            __builtin_memcpy(&bql[ks], &b, 16);
+        const float dm = h2f(p.dvmax[kvh]);
+        if (dm > 0.0f) {
+            int e;
+            (void)frexpf(dm, &e);
+            eshift = (float)(1 - e);
         }
     }
+    const int nh = (n >> 3) & 1;
 
-    floatx4 acc[16];  // O[row 4g+i][dim 16T + n]
+    // The two kinds of wave run separate code with the same barrier count:
+    // n_tiles + 1 in the loop, then two for the hand-over of m and l.
+    if (wave < kScoreWaves) {
+        const int w = wave;
+        float *ml = reinterpret_cast<float *>(smem + kLdsP) + w * (kRG * 32);  // [rg][row][m, l]
+        // Q codes of rows r = 32w + 16rg + n (position q_base + r / G, head
+        // kvh*G + r % G) as B operands, dims 32b + 8g..+7, and their d_q
+        half8 bq[kRG][8];
+        float qd[kRG][8];
+        int my_pos[kRG], m_off[kRG];
+        float m_run[kRG], l_part[kRG];
 #pragma unroll
-    for (int T = 0; T < 16; ++T) acc[T] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_part = 0.0f;
-
-    // Tile staging through registers: per thread 2 chunks (16 B) of each of
-    // Kh, Kl (32 keys x 512 B) and Vh, Vl (256 dims x 64 B).
-    uint4 pk[2], pkl[2], pv[2], pvl[2];
-    uint4 pmsk = make_uint4(0, 0, 0, 0);
-    int pre_nvalid = 0;
-    const bool mask_loader = p.mask && tid < QB * 4;  // 4 lanes x 8 keys per query position
-    const int mq = tid >> 2, mc = (tid & 3) * 8;
-    const bool mask_aligned = ((uintptr_t)p.mask % 16 == 0) && (p.mask_nb1 % 16 == 0);
-    const uint16_t *kf_h = p.kf + (int64_t)kvh * p.n_kv * kHeadDim;
-    const uint16_t *kfl_h = p.kfl + (int64_t)kvh * p.n_kv * kHeadDim;
-    const uint16_t *vt_h = p.vt + (int64_t)kvh * kHeadDim * p.n_kv_pad;
-    const uint16_t *vtl_h = p.vtl + (int64_t)kvh * kHeadDim * p.n_kv_pad;
-    auto load_tile = [&](int64_t kt, int nvalid) {
+        for (int rg = 0; rg < kRG; ++rg) {
+            const int r = 32 * w + 16 * rg + n;
+            const int pos = q_base + r / p.G;
+            my_pos[rg] = pos;
+            const bool ok = pos < p.n_q;
+            const uint32_t m = ok ? 0xffffffffu : 0u;
+            const int64_t row = (int64_t)(ok ? pos : 0) * p.H + kvh * p.G + r % p.G;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int c = tid + kThreads * i;  // 0..1023
-            const int key = c >> 5, col = c & 31;
-            const int64_t ko = (kt + (key < nvalid ? key : 0)) * kHeadDim + 8 * col;
-            pk[i] = *reinterpret_cast<const uint4 *>(kf_h + ko);
-            pkl[i] = *reinterpret_cast<const uint4 *>(kfl_h + ko);
-            const int dim = c >> 2, seg = c & 3;
-            const int64_t vo = (int64_t)dim * p.n_kv_pad + kt + 8 * seg;
-            pv[i] = *reinterpret_cast<const uint4 *>(vt_h + vo);
-            pvl[i] = *reinterpret_cast<const uint4 *>(vtl_h + vo);
-        }
-        if (p.mask && wave * 64 < QB * 4) {  // wave-uniform
-            const int qq = q_base + (mask_loader ? mq : 0);
-            const int64_t mrow = qq < p.n_q ? qq : 0;
-            const uint16_t *mp = reinterpret_cast<const uint16_t *>(p.mask + mrow * p.mask_nb1) + kt;
-            if (mask_aligned && nvalid == kPK) {  // uniform; stays in flight
-                pmsk = *reinterpret_cast<const uint4 *>(mp + mc);
-            } else {  // last tile of a range or unaligned rows: waits here
-                uint16_t e[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) e[j] = mp[mc + j < nvalid ? mc + j : 0];
-                __builtin_memcpy(&pmsk, e, 16);
+            for (int b = 0; b < 8; ++b) {
+                uint4 u = *reinterpret_cast<const uint4 *>(p.qc + row * kHeadDim + 32 * b + 8 * g);
+                u = make_uint4(u.x & m, u.y & m, u.z & m, u.w & m);
+                __builtin_memcpy(&bq[rg][b], &u, 16);
             }
+            const float4 d0 = *reinterpret_cast<const float4 *>(p.qd + row * 8);
+            const float4 d1 = *reinterpret_cast<const float4 *>(p.qd + row * 8 + 4);
+            qd[rg][0] = d0.x; qd[rg][1] = d0.y; qd[rg][2] = d0.z; qd[rg][3] = d0.w;
+            qd[rg][4] = d1.x; qd[rg][5] = d1.y; qd[rg][6] = d1.z; qd[rg][7] = d1.w;
+            const int pl = r / p.G;  // mask row of the position, keys 8g..8g+7
+            m_off[rg] = kLdsMask + 64 * pl + 16 * (g ^ ((pl >> 1) & 3));
+            m_run[rg] = -INFINITY;
+            l_part[rg] = 0.0f;
         }
-        pre_nvalid = nvalid;
-    };
-    auto store_tile = [&]() {
+        // K operand of key row 16kg + n, dims 32b + 8g..+7: chunk (4b + g) ^ (n & 7),
+        // halves swapped when n & 8; the XOR touches bit 2 of 4b + g, so even and odd
+        // b use two bases and b >> 1 adds 128 bytes.
+        int k_off[2][2];  // [b & 1][half]
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int c = tid + kThreads * i;
-            const int key = c >> 5, col = c & 31;
-            const bool ok = key < pre_nvalid;
-            *reinterpret_cast<uint4 *>(sK + key * kKRow + 16 * col) = keep_if(pk[i], ok);
-            *reinterpret_cast<uint4 *>(sKl + key * kKRow + 16 * col) = keep_if(pkl[i], ok);
-            const int dim = c >> 2, seg = c & 3;
-            *reinterpret_cast<uint4 *>(sV + dim * kVRow + 16 * seg) = keep_if(pv[i], true);
-            *reinterpret_cast<uint4 *>(sVl + dim * kVRow + 16 * seg) = keep_if(pvl[i], true);
-        }
-        if (mask_loader) *reinterpret_cast<uint4 *>(sM + mq * kPK + mc) = pmsk;
-    };
+        for (int bp = 0; bp < 2; ++bp)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) k_off[bp][hf] = n * 512 + 16 * ((4 * bp + g) ^ (n & 7)) + 8 * (hf ^ nh);
+        const int p_off = w * (kRG * 2048) + 16 * lane;  // P slots [w][rg][half][lane]
 
-    const int64_t n_tiles = k_end > k_begin ? (k_end - k_begin + kPK - 1) / kPK : 0;
-    if (n_tiles > 0) {
-        load_tile(k_begin, (int)(k_end - k_begin < kPK ? k_end - k_begin : kPK));
-        store_tile();
-    }
-    __syncthreads();
-
-    for (int64_t it = 0; it < n_tiles; ++it) {
-        const int64_t kt = k_begin + it * kPK;
-        const int nvalid = (int)(k_end - kt < kPK ? k_end - kt : kPK);
-        if (it + 1 < n_tiles) {
-            const int64_t kn = kt + kPK;
-            load_tile(kn, (int)(k_end - kn < kPK ? k_end - kn : kPK));
-        }
-        {
-            const int k0 = 0;
-            float s[2][4];
+        for (int t = 0; t <= n_tiles && n_tiles > 0; ++t) {
+            // this wave's DMAs landed; the barrier makes every wave's visible and
+            // retires the buffers the new DMAs overwrite
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            issue(t + 1 < n_tiles ? t + 1 : -1, t < n_tiles ? t : -1);
+            if (t == n_tiles) break;
+            const int64_t kt = k_begin + (int64_t)t * kPK;
+            const uint8_t *ks = smem + (t & 1) * kKStage;
+            const int nvalid = (int)(k_end - kt < kPK ? k_end - kt : kPK);
+            // this tile's four per-lane K bases, opaque to the compiler: every K read
+            // is then one of them plus an immediate offset (hoisting all 64
+            // base + offset sums out of the loop would need 64 more registers)
+            int kb[2][2];
 #pragma unroll
-            for (int st = 0; st < 2; ++st) {
-                floatx4 c = {0.f, 0.f, 0.f, 0.f};
-                const int koff = (k0 + 16 * st + n) * kKRow + 16 * g;
+            for (int bp = 0; bp < 2; ++bp)
 #pragma unroll
-                for (int ks = 0; ks < 8; ++ks) {
-                    const half8 a = *reinterpret_cast<const half8 *>(sK + koff + 64 * ks);
-                    const half8 al = *reinterpret_cast<const half8 *>(sKl + koff + 64 * ks);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bqh[ks], c, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bql[ks], c, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bqh[ks], c, 0, 0, 0);
+                for (int hf = 0; hf < 2; ++hf) {
+                    kb[bp][hf] = (t & 1) * kKStage + k_off[bp][hf];
+                    asm volatile("" : "+v"(kb[bp][hf]));
                 }
-                const int kc = k0 + 16 * st + 4 * g;
-                uint2 mraw = make_uint2(0, 0);
-                if (p.mask) mraw = *reinterpret_cast<const uint2 *>(sM + my_ql * kPK + kc);
-                const uint32_t mw[2] = {mraw.x, mraw.y};
+            // ---- S^T: sa[rg][kg][i] = S[key kt + 8g + 4kg + i][row n of group rg] ----
+            floatx4 sa[kRG][2];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int kl = kc + i;
-                    float sv = c[i] * p.scale;
-                    bool dead = kl >= nvalid;
-                    if (p.q_pos0 >= 0) {
-                        dead = dead || (kt + kl > p.q_pos0 + my_q);
-                    } else if (p.mask && row_ok) {
-                        const float mv = h2f((mw[i >> 1] >> (16 * (i & 1))) & 0xffff);
-                        dead = dead || (mv == -INFINITY);
-                        sv += mv;
+            for (int rg = 0; rg < kRG; ++rg) sa[rg][0] = sa[rg][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+#pragma unroll
+                for (int kg = 0; kg < 2; ++kg) {
+                    const int o = kg * 8192 + 128 * (b >> 1);
+                    const half8 ah = lds_half8(smem, kb[b & 1][0] + o, kb[b & 1][1] + o);
+                    const half8 al = lds_half8(smem, kb[b & 1][0] + o + kOffKl, kb[b & 1][1] + o + kOffKl);
+#pragma unroll
+                    for (int rg = 0; rg < kRG; ++rg) {
+                        floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[rg][b],
+                                                                           floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[rg][b], c, 0, 0, 0);
+                        sa[rg][kg] += qd[rg][b] * c;  // whole-vector: keeps sa one register tuple
                     }
-                    s[st][i] = dead ? -INFINITY : sv;
                 }
             }
-            float mt = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
-                             fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-            mt = fmaxf(mt, __shfl_xor(mt, 16));
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
-            const float m_new = fmaxf(m_run, mt);
-            const float mref = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = exp2f((m_run - mref) * kLog2e);
-            half8 pa;
-            float psum = 0.0f;
+            float s[kRG][8];  // keys 8g + jj, base-2 logits
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-                const float pr = exp2f((s[jj >> 2][jj & 3] - mref) * kLog2e);
-                psum += pr;
-                pa[jj] = (_Float16)pr;
+            for (int rg = 0; rg < kRG; ++rg)
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) s[rg][jj] = sa[rg][jj >> 2][jj & 3];
+            // ---- mask / causal / ragged tail ----------------------------------------
+            if (p.mask) {
+#pragma unroll
+                for (int rg = 0; rg < kRG; ++rg) {
+                    const uint4 mr = *reinterpret_cast<const uint4 *>(smem + m_off[rg] + (t & 1) * p.mask_stage);
+                    const uint32_t mw[4] = {mr.x, mr.y, mr.z, mr.w};
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj)
+                        s[rg][jj] = fmaf(h2f((mw[jj >> 1] >> (16 * (jj & 1))) & 0xffff), kLog2e, s[rg][jj]);
+                }
             }
-            l_part = l_part * alpha + psum;
-            m_run = m_new;
-            if (__any(alpha != 1.0f)) {
-                float ar[4];
+            if (nvalid < kPK || (p.q_pos0 >= 0 && kt + kPK - 1 > p.q_pos0 + q_base)) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * g + i);
+                for (int rg = 0; rg < kRG; ++rg) {
+                    int64_t lim = nvalid;  // keys at or past lim are dead for this row
+                    if (p.q_pos0 >= 0 && p.q_pos0 + my_pos[rg] + 1 - kt < lim) lim = p.q_pos0 + my_pos[rg] + 1 - kt;
 #pragma unroll
-                for (int T = 0; T < 16; ++T)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[T][i] *= ar[i];
+                    for (int jj = 0; jj < 8; ++jj) s[rg][jj] = 8 * g + jj < lim ? s[rg][jj] : -INFINITY;
+                }
             }
-            // O += P V: B[k][dim 16T+n], k = 8g+jj -> key 4g + jj (jj<4), 16 + 4g + jj-4
+            // ---- online softmax (base 2); P and the rescale factors to LDS -----------
+            uint8_t *pb = smem + kLdsP + (t & 1) * kPBuf + p_off;
+            float *ab = reinterpret_cast<float *>(smem + kLdsA + (t & 1) * kABuf) + w * (kRG * 16);
 #pragma unroll
-            for (int T = 0; T < 16; ++T) {
-                const int vo = (16 * T + n) * kVRow + 2 * (k0 + 4 * g);
-                const uint2 b0 = *reinterpret_cast<const uint2 *>(sV + vo);
-                const uint2 b1 = *reinterpret_cast<const uint2 *>(sV + vo + 32);
-                const uint2 c0 = *reinterpret_cast<const uint2 *>(sVl + vo);
-                const uint2 c1 = *reinterpret_cast<const uint2 *>(sVl + vo + 32);
-                const uint4 bb = make_uint4(b0.x, b0.y, b1.x, b1.y);
-                const uint4 cc = make_uint4(c0.x, c0.y, c1.x, c1.y);
-                half8 bv, bvl;
-                __builtin_memcpy(&bv, &bb, 16);
-                __builtin_memcpy(&bvl, &cc, 16);
-                acc[T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, bv, acc[T], 0, 0, 0);
-                acc[T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, bvl, acc[T], 0, 0, 0);
+            for (int rg = 0; rg < kRG; ++rg) {
+                float alpha = 1.0f;
+                bool over = false;
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) over |= s[rg][jj] > m_run[rg];
+                if (__any(over)) {
+                    float mt = fmaxf(fmaxf(fmaxf(s[rg][0], s[rg][1]), fmaxf(s[rg][2], s[rg][3])),
+                                     fmaxf(fmaxf(s[rg][4], s[rg][5]), fmaxf(s[rg][6], s[rg][7])));
+                    mt = fmaxf(mt, __shfl_xor(mt, 16));
+                    mt = fmaxf(mt, __shfl_xor(mt, 32));
+                    const float m_new = fmaxf(m_run[rg], mt);
+                    alpha = m_run[rg] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[rg] - m_new);
+                    l_part[rg] *= alpha;
+                    m_run[rg] = m_new;
+                }
+                const float mref = (m_run[rg] == -INFINITY ? 0.0f : m_run[rg]) - eshift;
+                float pf[8], psum = 0.0f;
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    pf[jj] = __builtin_amdgcn_exp2f(s[rg][jj] - mref);
+                    psum += pf[jj];
+                }
+                l_part[rg] += psum;
+                *reinterpret_cast<float4 *>(pb + rg * 2048) = make_float4(pf[0], pf[1], pf[2], pf[3]);
+                *reinterpret_cast<float4 *>(pb + rg * 2048 + 1024) = make_float4(pf[4], pf[5], pf[6], pf[7]);
+                if (g == 0) ab[rg * 16 + n] = alpha;
+            }
+        }
+        // ---- hand m and l of the rows to the value waves ----------------------------
+        __syncthreads();
+        if (n_tiles > 0) {
+#pragma unroll
+            for (int rg = 0; rg < kRG; ++rg) {
+                float lp = l_part[rg];
+                lp += __shfl_xor(lp, 16);
+                lp += __shfl_xor(lp, 32);
+                if (g == 0) {
+                    ml[rg * 32 + 2 * n] = m_run[rg];
+                    ml[rg * 32 + 2 * n + 1] = lp;
+                }
             }
         }
         __syncthreads();
-        if (it + 1 < n_tiles) store_tile();
-        __syncthreads();
+        return;
     }
 
-    // ---- epilogue: each wave owns its 16 rows
-    l_part += __shfl_xor(l_part, 16);
-    l_part += __shfl_xor(l_part, 32);
-    float lrow[4], mrow[4];
-    int qrow[4], hrow[4];
+    // ---- value waves: O[row 32w + 16rg + 4g + i][dim 16T + n] ----------------
+    const int w = wave - kScoreWaves;
+    const float *ml = reinterpret_cast<const float *>(smem + kLdsP) + w * (kRG * 32);  // [rg][row][m, l]
+    // V operand of dim 16T + n, keys 8g..8g+7: chunk g ^ ((n >> 1) & 3), halves swapped when n & 8.
+    const int v_off0 = 64 * n + 16 * (g ^ ((n >> 1) & 3)) + 8 * nh;
+    const int v_off1 = v_off0 ^ 8;
+    const int p_off = w * (kRG * 2048) + 16 * lane;
+    floatx4 acc[kRG][16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        lrow[i] = __shfl(l_part, 4 * g + i);
-        mrow[i] = __shfl(m_run, 4 * g + i);
-        qrow[i] = q_base + wave * QW + (4 * g + i) / p.G;
-        hrow[i] = kvh * p.G + (4 * g + i) % p.G;
-    }
-    const int rows_total = p.n_q * p.H;
-    if (p.n_splits == 1) {
+    for (int rg = 0; rg < kRG; ++rg)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (qrow[i] >= p.n_q) continue;
-            const int64_t r = (int64_t)qrow[i] * p.H + hrow[i];
-            const float inv = lrow[i] == 0.0f ? 0.0f : 1.0f / lrow[i];
+        for (int T = 0; T < 16; ++T) acc[rg][T] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t <= n_tiles && n_tiles > 0; ++t) {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        issue(t + 1 < n_tiles ? t + 1 : -1, t < n_tiles ? t : -1);
+        if (t == 0) continue;
+        const int tp = t - 1;
+        const uint8_t *vs = smem + kLdsV + (tp & 1) * kVStage;
+        // this tile's two per-lane V bases, opaque to the compiler (see the K reads)
+        int vb0 = kLdsV + (tp & 1) * kVStage + v_off0, vb1 = kLdsV + (tp & 1) * kVStage + v_off1;
+        asm volatile("" : "+v"(vb0), "+v"(vb1));
+        const uint8_t *pb = smem + kLdsP + (tp & 1) * kPBuf + p_off;
+        const float *ab = reinterpret_cast<const float *>(smem + kLdsA + (tp & 1) * kABuf) + w * (kRG * 16);
+        float pf[kRG][8];
+        floatx4 a4[kRG];  // rescale factors of rows 4g..4g+3 (exactly 1 where no maximum grew)
 #pragma unroll
-            for (int T = 0; T < 16; ++T) {
-                float o = acc[T][i] * inv;
-                if (p.gate) {
-                    const float gv = reinterpret_cast<const float *>(p.gate + qrow[i] * p.gate_nb2 +
-                                                                     hrow[i] * p.gate_nb1)[16 * T + n];
-                    o = o * (1.0f / (1.0f + expf(-gv)));
-                }
-                p.dst[r * kHeadDim + 16 * T + n] = o;
+        for (int rg = 0; rg < kRG; ++rg) {
+            a4[rg] = *reinterpret_cast<const floatx4 *>(ab + rg * 16 + 4 * g);
+            const float4 p0 = *reinterpret_cast<const float4 *>(pb + rg * 2048);
+            const float4 p1 = *reinterpret_cast<const float4 *>(pb + rg * 2048 + 1024);
+            pf[rg][0] = p0.x; pf[rg][1] = p0.y; pf[rg][2] = p0.z; pf[rg][3] = p0.w;
+            pf[rg][4] = p1.x; pf[rg][5] = p1.y; pf[rg][6] = p1.z; pf[rg][7] = p1.w;
+        }
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            half8 dvb;
+            {
+                const uint4 u = *reinterpret_cast<const uint4 *>(vs + kOffDv + 64 * b + 16 * g);
+                __builtin_memcpy(&dvb, &u, 16);
+            }
+            half8 a[kRG];
+#pragma unroll
+            for (int rg = 0; rg < kRG; ++rg)
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) a[rg][jj] = (_Float16)__builtin_fmaf(pf[rg][jj], (float)dvb[jj], 0.0f);
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int T = 2 * b + hf;
+                const half8 bv = lds_half8(smem, vb0 + 1024 * T, vb1 + 1024 * T);
+                // O = alpha O + P V; the product is applied unconditionally (exact
+                // for alpha = 1): a conditional rescale makes the compiler keep a
+                // second copy of O and spill
+#pragma unroll
+                for (int rg = 0; rg < kRG; ++rg)
+                    acc[rg][T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rg], bv, acc[rg][T] * a4[rg], 0, 0, 0);
             }
         }
-    } else {
+    }
+    __syncthreads();  // m and l of the rows ...
+    __syncthreads();  // ... are in LDS
+    const int rows_total = p.n_q * p.H;
+#pragma unroll
+    for (int rg = 0; rg < kRG; ++rg) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if (qrow[i] >= p.n_q) continue;
-            const int64_t r = (int64_t)qrow[i] * p.H + hrow[i];
-            float *pa = p.part_acc + ((int64_t)split * rows_total + r) * kHeadDim;
+            const int r = 32 * w + 16 * rg + 4 * g + i;
+            const int qrow = q_base + r / p.G, hrow = kvh * p.G + r % p.G;
+            if (qrow >= p.n_q) continue;
+            const float mrow = n_tiles > 0 ? ml[rg * 32 + 2 * (4 * g + i)] : -INFINITY;
+            const float lrow = n_tiles > 0 ? ml[rg * 32 + 2 * (4 * g + i) + 1] : 0.0f;
+            const int64_t ridx = (int64_t)qrow * p.H + hrow;
+            if (p.n_splits == 1) {
+                const float inv = lrow == 0.0f ? 0.0f : 1.0f / lrow;
 #pragma unroll
-            for (int T = 0; T < 16; ++T) pa[16 * T + n] = acc[T][i];
-            if (n == 0) {
-                p.part_ml[((int64_t)split * rows_total + r) * 2] = mrow[i];
-                p.part_ml[((int64_t)split * rows_total + r) * 2 + 1] = lrow[i];
+                for (int T = 0; T < 16; ++T) {
+                    float o = acc[rg][T][i] * inv;
+                    if (p.gate) {
+                        const float gv = reinterpret_cast<const float *>(p.gate + qrow * p.gate_nb2 +
+                                                                         hrow * p.gate_nb1)[16 * T + n];
+                        o = o * (1.0f / (1.0f + expf(-gv)));
+                    }
+                    p.dst[ridx * kHeadDim + 16 * T + n] = o;
+                }
+            } else {
+                float *pa_out = p.part_acc + ((int64_t)split * rows_total + ridx) * kHeadDim;
+#pragma unroll
+                for (int T = 0; T < 16; ++T) pa_out[16 * T + n] = acc[rg][T][i];
+                if (n == 0) {
+                    // the combine works in base e: m * ln 2 (acc and l of every split
+                    // carry the same 2^e, which cancels in the merge)
+                    p.part_ml[((int64_t)split * rows_total + ridx) * 2] =
+                        mrow == -INFINITY ? mrow : mrow * 0.6931471805599453f;
+                    p.part_ml[((int64_t)split * rows_total + ridx) * 2 + 1] = lrow;
+                }
             }
         }
     }
 }
 
-constexpr size_t kLdsBytes = 2 * (size_t)kPK * kKRow + 2 * (size_t)kHeadDim * kVRow + (size_t)kMaxQ * kPK * 2;
-
 size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct PrefillPlan {
-    int64_t n_kv_pad;
-    int q_tiles, n_splits;
+    int64_t kv_tiles;
+    int qb, q_tiles, n_splits, mask_stage;
     int64_t split_len;
-    size_t off_kf, off_kfl, off_vt, off_vtl, off_qh, off_ql, off_pa, off_pm, total;
+    size_t off_kv, off_dvmax, off_qc, off_qd, off_mask, off_pa, off_pm, total;
 };
 
 PrefillPlan plan(int64_t n_q, int64_t H, int64_t Hkv, int64_t n_kv) {
     PrefillPlan pl{};
     const int G = (int)(H / Hkv);
-    const int QB = (16 / G) * kWaves;
-    pl.n_kv_pad = (n_kv + 63) / 64 * 64;  // vdeq writes 64-key groups
-    pl.q_tiles = (int)((n_q + QB - 1) / QB);
+    pl.qb = kRowsPerWG / G;
+    pl.mask_stage = pl.qb * kPK * 2;
+    pl.kv_tiles = (n_kv + 63) / 64 * 2;  // vdeq writes 64-key groups
+    pl.q_tiles = (int)((n_q + pl.qb - 1) / pl.qb);
     const int64_t wgs = (int64_t)pl.q_tiles * Hkv;
     const int64_t cus = device_cu_count();
     int64_t splits = (cus + wgs - 1) / wgs;
-    const int64_t max_by_len = (n_kv + 1023) / 1024;  // at least ~1024 keys per split
+    const int64_t max_by_len = (n_kv + 511) / 512;  // at least ~512 keys per split
     if (splits > max_by_len) splits = max_by_len;
     if (splits < 1) splits = 1;
     pl.split_len = ((n_kv + splits - 1) / splits + kPK - 1) / kPK * kPK;
     pl.n_splits = (int)((n_kv + pl.split_len - 1) / pl.split_len);
     size_t o = 0;
-    pl.off_kf = o; o = al256(o + (size_t)Hkv * n_kv * kHeadDim * 2);
-    pl.off_kfl = o; o = al256(o + (size_t)Hkv * n_kv * kHeadDim * 2);
-    pl.off_vt = o; o = al256(o + (size_t)Hkv * kHeadDim * pl.n_kv_pad * 2);
-    pl.off_vtl = o; o = al256(o + (size_t)Hkv * kHeadDim * pl.n_kv_pad * 2);
-    pl.off_qh = o; o = al256(o + (size_t)n_q * H * kHeadDim * 2);
-    pl.off_ql = o; o = al256(o + (size_t)n_q * H * kHeadDim * 2);
+    pl.off_kv = o; o = al256(o + (size_t)Hkv * pl.kv_tiles * kTileBytes);
+    pl.off_dvmax = o; o = al256(o + (size_t)Hkv * 4);
+    pl.off_qc = o; o = al256(o + (size_t)n_q * H * kHeadDim * 2);
+    pl.off_qd = o; o = al256(o + (size_t)n_q * H * 8 * 4);
+    pl.off_mask = o; o = al256(o + (size_t)n_q * ((n_kv + 7) / 8 * 8) * 2);
     pl.off_pa = o;
     pl.off_pm = o;
     if (pl.n_splits > 1) {
@@ -529,48 +706,74 @@ int launch_fa_prefill(const FaArgs &a, hipStream_t s) {
         return set_error(SQA_ERR_WORKSPACE, "flash_attn_ext: workspace %zu bytes < %zu needed", a.ws_bytes,
                          pl.total);
     uint8_t *base = reinterpret_cast<uint8_t *>(((uintptr_t)a.ws + 255) & ~(uintptr_t)255);
-    uint16_t *kf = reinterpret_cast<uint16_t *>(base + pl.off_kf);
-    uint16_t *kfl = reinterpret_cast<uint16_t *>(base + pl.off_kfl);
-    uint16_t *vt = reinterpret_cast<uint16_t *>(base + pl.off_vt);
-    uint16_t *vtl = reinterpret_cast<uint16_t *>(base + pl.off_vtl);
-    uint16_t *qh = reinterpret_cast<uint16_t *>(base + pl.off_qh);
-    uint16_t *ql = reinterpret_cast<uint16_t *>(base + pl.off_ql);
+    uint8_t *kv = base + pl.off_kv;
+    uint32_t *dvmax = reinterpret_cast<uint32_t *>(base + pl.off_dvmax);
+    uint16_t *qc = reinterpret_cast<uint16_t *>(base + pl.off_qc);
+    float *qd = reinterpret_cast<float *>(base + pl.off_qd);
+
+    PrefillParams p;
+    p.mask = nullptr;
+    p.mask_nb1 = 0;
+    p.mask_len = 0;
+    const char *mask_src = nullptr;
+    int64_t mask_src_nb1 = 0;
+    if (a.q_pos0 < 0 && a.mask) {
+        mask_src = (const char *)a.mask->data;
+        mask_src_nb1 = (int64_t)a.mask->nb[1];
+        if ((uintptr_t)mask_src % 16 == 0 && mask_src_nb1 % 16 == 0 && n_kv % 8 == 0) {
+            p.mask = mask_src;
+            p.mask_nb1 = mask_src_nb1;
+            p.mask_len = n_kv;
+            mask_src = nullptr;
+        } else {
+            const int64_t len8 = (n_kv + 7) / 8 * 8;
+            p.mask = (const char *)(base + pl.off_mask);
+            p.mask_nb1 = len8 * 2;
+            p.mask_len = len8;
+        }
+        // the mask DMA addresses rows with 32-bit offsets
+        if ((n_q - 1) * p.mask_nb1 + p.mask_len * 2 > (int64_t)UINT32_MAX)
+            return set_error(SQA_ERR_UNSUPPORTED, "prefill: mask of %lld rows x %lld bytes exceeds 4 GiB",
+                             (long long)n_q, (long long)p.mask_nb1);
+    }
 
     int prof = profile_start("fa_prefill_prep", s);
     {
-        const int64_t nk = n_kv * Hkv * kBlocksPerHead;
+        const int64_t nk = pl.kv_tiles * kPK * Hkv * kBlocksPerHead;
         kdeq_kernel<<<dim3((unsigned)((nk + 255) / 256)), dim3(256), 0, s>>>(
-            (const uint8_t *)k.data, (int64_t)k.nb[1], (int64_t)k.nb[2], n_kv, (int)Hkv, kf, kfl);
-        vdeq_kernel<<<dim3((unsigned)(pl.n_kv_pad / 64), (unsigned)Hkv), dim3(256), 0, s>>>(
-            (const uint8_t *)v.data, (int64_t)v.nb[1], (int64_t)v.nb[2], n_kv, pl.n_kv_pad, vt, vtl);
+            (const uint8_t *)k.data, (int64_t)k.nb[1], (int64_t)k.nb[2], n_kv, pl.kv_tiles, (int)Hkv, kv, dvmax);
+        vdeq_kernel<<<dim3((unsigned)(pl.kv_tiles / 2), (unsigned)Hkv), dim3(256), 0, s>>>(
+            (const uint8_t *)v.data, (int64_t)v.nb[1], (int64_t)v.nb[2], n_kv, pl.kv_tiles, kv, dvmax);
         const int64_t nqb = n_q * H * kBlocksPerHead;
         qprep_kernel<<<dim3((unsigned)((nqb + 255) / 256)), dim3(256), 0, s>>>(
-            (const char *)q.data, (int64_t)q.nb[1], (int64_t)q.nb[2], (int)n_q, (int)H, qh, ql);
+            (const char *)q.data, (int64_t)q.nb[1], (int64_t)q.nb[2], (int)n_q, (int)H, a.scale * kLog2e, qc, qd);
+        if (mask_src) {
+            int64_t grid = (p.mask_len * n_q + 255) / 256;
+            if (grid > 2048) grid = 2048;
+            pf_mask_pack_kernel<<<dim3((unsigned)grid), dim3(256), 0, s>>>(
+                mask_src, mask_src_nb1, n_kv, (int)n_q, p.mask_len, (uint16_t *)(base + pl.off_mask));
+        }
     }
     profile_stop(prof, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_status(e, "prefill pre-pass launch");
 
-    PrefillParams p;
-    p.kf = kf;
-    p.kfl = kfl;
-    p.vt = vt;
-    p.vtl = vtl;
-    p.qhi = qh;
-    p.qlo = ql;
+    p.kv = kv;
+    p.dvmax = dvmax;
+    p.qc = qc;
+    p.qd = qd;
     p.n_kv = n_kv;
-    p.n_kv_pad = pl.n_kv_pad;
+    p.kv_tiles = pl.kv_tiles;
     p.n_q = (int)n_q;
     p.H = (int)H;
     p.G = G;
     p.Hkv = (int)Hkv;
-    p.mask = (a.q_pos0 < 0 && a.mask) ? (const char *)a.mask->data : nullptr;
-    p.mask_nb1 = a.mask ? (int64_t)a.mask->nb[1] : 0;
     p.q_pos0 = a.q_pos0;
-    p.scale = a.scale;
     p.n_splits = pl.n_splits;
     p.q_tiles = pl.q_tiles;
     p.split_len = pl.split_len;
+    p.qb = pl.qb;
+    p.mask_stage = pl.mask_stage;
     p.part_acc = reinterpret_cast<float *>(base + pl.off_pa);
     p.part_ml = reinterpret_cast<float *>(base + pl.off_pm);
     p.dst = (float *)a.dst->data;
@@ -578,15 +781,16 @@ int launch_fa_prefill(const FaArgs &a, hipStream_t s) {
     p.gate_nb1 = a.gate ? (int64_t)a.gate->nb[1] : 0;
     p.gate_nb2 = a.gate ? (int64_t)a.gate->nb[2] : 0;
 
-    static bool lds_ok = false;
-    if (!lds_ok) {
+    const int lds_bytes = kLdsMask + (p.mask ? 2 * pl.mask_stage : 0);
+    static int lds_set = 0;
+    if (lds_bytes > lds_set) {
         e = hipFuncSetAttribute((const void *)fa_prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)kLdsBytes);
+                                lds_bytes);
         if (e != hipSuccess) return hip_status(e, "fa_prefill LDS attribute");
-        lds_ok = true;
+        lds_set = lds_bytes;
     }
     prof = profile_start("fa_prefill", s);
-    fa_prefill_kernel<<<dim3((unsigned)(pl.q_tiles * Hkv * pl.n_splits)), dim3(kThreads), kLdsBytes, s>>>(p);
+    fa_prefill_kernel<<<dim3((unsigned)(pl.q_tiles * Hkv * pl.n_splits)), dim3(kThreads), lds_bytes, s>>>(p);
     profile_stop(prof, s);
     e = hipGetLastError();
     if (e != hipSuccess) return hip_status(e, "fa_prefill launch");

@@ -62,3 +62,20 @@ def test_prefill_fully_masked_rows_are_zero(sqa, orc, dev):
     got = run_gpu(sqa, dev, q, kq, vq, mask)
     assert np.all(got[5] == 0)
     assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("n_q", [2, 64])
+def test_rising_logits_force_rescales(sqa, orc, dev, n_q):
+    """A mask rising by 0.05 per key (natural-log units) lifts the running
+    maximum every few tiles, so the online softmax rescales its accumulator
+    many times (the decode kernel for n_q = 2, the prefill kernel for 64)."""
+    n_kv = 3000
+    q, kq, vq = qkv(orc, 77 + n_q, n_q, n_kv)
+    causal = orc.causal_mask(n_q, n_kv, n_kv - n_q).astype(np.float32)
+    ramp = np.arange(n_kv, dtype=np.float32) * np.float32(0.05)
+    mask = (causal + ramp[None, :]).astype(np.float16)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    err = rel_err(got, ref)
+    print(f"rising logits n_q={n_q}: max err / rms = {err:.3e}")
+    assert err <= TOL
