@@ -93,11 +93,10 @@ int check_fa(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
     if ((uintptr_t)dst->data % 16)
         return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: dst data must be 16-byte aligned");
     const int64_t G = q->ne[2] / k->ne[2];
-    *decode = q->ne[1] * G <= 16;
-    if (*decode && k->ne[2] != 2)
-        return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: decode kernel needs n_head_kv == 2");
-    if (*decode && ((uintptr_t)q->data % 16 || q->nb[1] % 16 || q->nb[2] % 16))
-        return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: q rows must be 16-byte aligned");
+    const bool q_aligned = (uintptr_t)q->data % 16 == 0 && q->nb[1] % 16 == 0 && q->nb[2] % 16 == 0;
+    // the split-KV decode kernel: up to 4 positions and 16 query rows per KV head,
+    // two KV heads, 16-byte aligned q rows; everything else runs as a prefill chunk
+    *decode = q->ne[1] <= 4 && q->ne[1] * G <= 16 && k->ne[2] == 2 && q_aligned;
     if (!*decode && 16 % G != 0)
         return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: prefill needs n_head/n_head_kv to divide 16");
     return SQA_OK;

@@ -108,106 +108,111 @@ __device__ __forceinline__ void split_hl(float x, uint16_t &hi, uint16_t &lo) {
     __builtin_memcpy(&lo, &l, 2);
 }
 
-// One thread per q4_0 block of K (zeros for keys past n_kv): 18 bytes in,
-// 32 fp16 Kh + 32 fp16 Kl out, as 4 + 4 swizzled 16-byte chunks of the key's row.
-// Thread 0 also clears the per-head |d_v| maxima that vdeq accumulates.
-__global__ __launch_bounds__(256) void kdeq_kernel(const uint8_t *__restrict__ k, int64_t nb1, int64_t nb2,
-                                                   int64_t n_kv, int64_t kv_tiles, int hkv,
-                                                   uint8_t *__restrict__ kv, uint32_t *__restrict__ dvmax) {
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (gid < hkv) dvmax[gid] = 0;
-    if (gid >= kv_tiles * kPK * hkv * kBlocksPerHead) return;
-    const int b = (int)(gid % kBlocksPerHead);
-    const int64_t kh = gid / kBlocksPerHead;  // key * hkv + head
-    const int h = (int)(kh % hkv);
-    const int64_t key = kh / hkv;
-    const bool ok = key < n_kv;
-    const uint16_t *src = reinterpret_cast<const uint16_t *>(k + (ok ? key : 0) * nb1 + h * nb2 + 18 * b);
-    const float d = ok ? h2f(src[0]) : 0.0f;
-    uint16_t out[32], outl[32];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t two = src[1 + j];  // qs[2j], qs[2j+1]
-        const int b0 = two & 0xff, b1 = two >> 8;
-        split_hl((float)((b0 & 15) - 8) * d, out[2 * j], outl[2 * j]);
-        split_hl((float)((b1 & 15) - 8) * d, out[2 * j + 1], outl[2 * j + 1]);
-        split_hl((float)((b0 >> 4) - 8) * d, out[16 + 2 * j], outl[16 + 2 * j]);
-        split_hl((float)((b1 >> 4) - 8) * d, out[16 + 2 * j + 1], outl[16 + 2 * j + 1]);
-    }
-    const int r = key_row((int)(key & (kPK - 1)));
-    uint8_t *row = kv + ((int64_t)h * kv_tiles + (key >> 5)) * kTileBytes + r * 512;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int pos = (4 * b + j) ^ (r & 7);
-        uint4 v, w;
-        __builtin_memcpy(&v, out + 8 * j, 16);
-        __builtin_memcpy(&w, outl + 8 * j, 16);
-        *reinterpret_cast<uint4 *>(row + 16 * pos) = swap_halves(v, r & 8);
-        *reinterpret_cast<uint4 *>(row + kOffKl + 16 * pos) = swap_halves(w, r & 8);
-    }
-}
-
-// One workgroup per (64 keys, head): thread t handles keys 8*(t%8)..+7 (one
-// 16-byte chunk of a Vc row) of the 8 dims {32beta + 4w + j, 32beta + 16 + 4w + j}
-// (beta = t/32, w = (t/8)%4); threads with w == 0 also write the 8 keys' d_v of
-// block beta. Keys past n_kv get zero codes and scales. Each wavefront folds
-// the largest |d_v| it saw into dvmax[head] (fp16 magnitude bits).
-__global__ __launch_bounds__(256) void vdeq_kernel(const uint8_t *__restrict__ v, int64_t nb1, int64_t nb2,
-                                                   int64_t n_kv, int64_t kv_tiles, uint8_t *__restrict__ kv,
-                                                   uint32_t *__restrict__ dvmax) {
+// One workgroup per (64 keys, KV head): the 64 q4_0 rows of K and of V are
+// staged in LDS with 16-byte loads (zeros past n_kv), then
+//   K: thread t takes blocks (key, b) = t and t + 256 (key = idx / 8, b = idx % 8):
+//      32 fp16 Kh + 32 fp16 Kl as 4 + 4 swizzled 16-byte chunks of the key's row;
+//   V: thread t writes the Vc row of dim t (32 codes, 64 bytes) of both tiles;
+//      threads 0..15 write the Dv rows and fold the largest |d_v| into
+//      dvmax[head] (fp16 magnitude bits, cleared by qprep_kernel, which runs
+//      first).
+__global__ __launch_bounds__(256) void kvprep_kernel(const uint8_t *__restrict__ k, int64_t k_nb1, int64_t k_nb2,
+                                                     const uint8_t *__restrict__ v, int64_t v_nb1, int64_t v_nb2,
+                                                     int64_t n_kv, int64_t kv_tiles, uint8_t *__restrict__ kv,
+                                                     uint32_t *__restrict__ dvmax) {
+    __shared__ __align__(16) uint8_t sk[64 * kHeadRowBytes], sv[64 * kHeadRowBytes];
     const int t = threadIdx.x;
     const int h = blockIdx.y;
-    const int64_t k0 = (int64_t)blockIdx.x * 64 + 8 * (t & 7);
-    const int beta = t >> 5;
-    const int w = (t >> 3) & 3;
-    uint16_t lo[8][4], hi[8][4], dd[8];  // [key][j]
-    uint32_t dmax = 0;
+    const int64_t k0 = (int64_t)blockIdx.x * 64;
+    for (int idx = t; idx < 64 * 9; idx += 256) {  // 9 x 16 bytes per 144-byte row
+        const int key = idx / 9, c = idx - 9 * key;
+        uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
+        if (k0 + key < n_kv) {
+            a = *reinterpret_cast<const uint4 *>(k + (k0 + key) * k_nb1 + h * k_nb2 + 16 * c);
+            b = *reinterpret_cast<const uint4 *>(v + (k0 + key) * v_nb1 + h * v_nb2 + 16 * c);
+        }
+        *reinterpret_cast<uint4 *>(sk + kHeadRowBytes * key + 16 * c) = a;
+        *reinterpret_cast<uint4 *>(sv + kHeadRowBytes * key + 16 * c) = b;
+    }
+    __syncthreads();
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-        const int64_t key = k0 + kk;
-        const bool ok = key < n_kv;
-        const uint16_t *blk = reinterpret_cast<const uint16_t *>(v + (ok ? key : 0) * nb1 + h * nb2 + 18 * beta);
-        dd[kk] = ok ? blk[0] : 0;
-        const uint32_t mag = dd[kk] & 0x7fffu;
-        dmax = mag > dmax ? mag : dmax;
-        const uint32_t q01 = blk[1 + 2 * w], q23 = blk[2 + 2 * w];
-        const uint32_t x = ok ? (q01 | (q23 << 16)) : 0x88888888u;  // qs[4w..4w+3]; code 8 -> 0
+    for (int i = 0; i < 2; ++i) {
+        const int idx = t + 256 * i;
+        const int key = idx >> 3, b = idx & 7;
+        const uint16_t *src = reinterpret_cast<const uint16_t *>(sk + kHeadRowBytes * key + 18 * b);
+        const float d = h2f(src[0]);
+        uint16_t out[32], outl[32];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t two = src[1 + j];  // qs[2j], qs[2j+1]
+            const int b0 = two & 0xff, b1 = two >> 8;
+            split_hl((float)((b0 & 15) - 8) * d, out[2 * j], outl[2 * j]);
+            split_hl((float)((b1 & 15) - 8) * d, out[2 * j + 1], outl[2 * j + 1]);
+            split_hl((float)((b0 >> 4) - 8) * d, out[16 + 2 * j], outl[16 + 2 * j]);
+            split_hl((float)((b1 >> 4) - 8) * d, out[16 + 2 * j + 1], outl[16 + 2 * j + 1]);
+        }
+        const int64_t gkey = k0 + key;
+        const int r = key_row((int)(gkey & (kPK - 1)));
+        uint8_t *row = kv + ((int64_t)h * kv_tiles + (gkey >> 5)) * kTileBytes + r * 512;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int byte = (x >> (8 * j)) & 0xff;
-            const _Float16 l = (_Float16)((byte & 15) - 8), u = (_Float16)((byte >> 4) - 8);
-            __builtin_memcpy(&lo[kk][j], &l, 2);
-            __builtin_memcpy(&hi[kk][j], &u, 2);
+            const int pos = (4 * b + j) ^ (r & 7);
+            uint4 x, y;
+            __builtin_memcpy(&x, out + 8 * j, 16);
+            __builtin_memcpy(&y, outl + 8 * j, 16);
+            *reinterpret_cast<uint4 *>(row + 16 * pos) = swap_halves(x, r & 8);
+            *reinterpret_cast<uint4 *>(row + kOffKl + 16 * pos) = swap_halves(y, r & 8);
         }
     }
-    uint8_t *vrec = kv + ((int64_t)h * kv_tiles + (k0 >> 5)) * kTileBytes + kKHalf;
-    const int c = (int)((k0 & (kPK - 1)) >> 3);  // chunk of the Vc row
+    // V: thread t writes the Vc row of dim t (its 32 keys' codes, 64 bytes) of
+    // both tiles; threads 0..15 also write the Dv row of (tile t / 8, block t % 8)
+    {
+        const int d = t, beta = d >> 5, e = d & 31;
+        const int boff = 18 * beta + 2 + (e & 15), shift = 4 * (e >> 4);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        uint16_t row_lo[8], row_hi[8];
+        for (int u = 0; u < 2; ++u) {
+            uint16_t codes[32];
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-            row_lo[kk] = lo[kk][j];
-            row_hi[kk] = hi[kk][j];
+            for (int kk = 0; kk < 32; ++kk) {
+                const int nib = (sv[kHeadRowBytes * (32 * u + kk) + boff] >> shift) & 15;
+                const _Float16 cv = (_Float16)(nib - 8);
+                __builtin_memcpy(&codes[kk], &cv, 2);
+            }
+            uint8_t *vrec = kv + ((int64_t)h * kv_tiles + ((k0 >> 5) + u)) * kTileBytes + kKHalf;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {  // keys 8c..8c+7 at chunk c ^ ((d >> 1) & 3), halves swapped when d & 8
+                uint4 x;
+                __builtin_memcpy(&x, codes + 8 * c, 16);
+                *reinterpret_cast<uint4 *>(vrec + 64 * d + 16 * (c ^ ((d >> 1) & 3))) = swap_halves(x, d & 8);
+            }
         }
-        const int dlo = 32 * beta + 4 * w + j, dhi = dlo + 16;
-        uint4 a, b;
-        __builtin_memcpy(&a, row_lo, 16);
-        __builtin_memcpy(&b, row_hi, 16);
-        *reinterpret_cast<uint4 *>(vrec + 64 * dlo + 16 * (c ^ ((dlo >> 1) & 3))) = swap_halves(a, dlo & 8);
-        *reinterpret_cast<uint4 *>(vrec + 64 * dhi + 16 * (c ^ ((dhi >> 1) & 3))) = swap_halves(b, dhi & 8);
-    }
-    if (w == 0) {
-        uint4 a;
-        __builtin_memcpy(&a, dd, 16);
-        *reinterpret_cast<uint4 *>(vrec + kOffDv + 64 * beta + 16 * c) = a;
-    }
+        uint32_t dmax = 0;
+        if (t < 16) {
+            const int u = t >> 3, b = t & 7;
+            uint16_t dd[32];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const uint32_t other = (uint32_t)__shfl_xor((int)dmax, o);
-        dmax = other > dmax ? other : dmax;
+            for (int kk = 0; kk < 32; ++kk) {
+                dd[kk] = *reinterpret_cast<const uint16_t *>(sv + kHeadRowBytes * (32 * u + kk) + 18 * b);
+                const uint32_t mag = dd[kk] & 0x7fffu;
+                dmax = mag > dmax ? mag : dmax;
+            }
+            uint8_t *vrec = kv + ((int64_t)h * kv_tiles + ((k0 >> 5) + u)) * kTileBytes + kKHalf;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                uint4 x;
+                __builtin_memcpy(&x, dd + 8 * c, 16);
+                *reinterpret_cast<uint4 *>(vrec + kOffDv + 64 * b + 16 * c) = x;
+            }
+        }
+        if (t < 64) {
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                const uint32_t other = (uint32_t)__shfl_xor((int)dmax, o);
+                dmax = other > dmax ? other : dmax;
+            }
+            if (t == 0) atomicMax(dvmax + h, dmax);
+        }
     }
-    if ((t & 63) == 0) atomicMax(dvmax + h, dmax);
 }
 
 // One thread per 32-value block of one (query, head) row: q8_0 with ggml's x86
@@ -215,8 +220,10 @@ __global__ __launch_bounds__(256) void vdeq_kernel(const uint8_t *__restrict__ v
 // (exact integers) and fp16(d) * scale * log2(e) as f32.
 __global__ __launch_bounds__(256) void qprep_kernel(const char *__restrict__ q, int64_t nb1, int64_t nb2,
                                                     int n_q, int H, float qscale, uint16_t *__restrict__ qc,
-                                                    float *__restrict__ qd) {
+                                                    float *__restrict__ qd, uint32_t *__restrict__ dvmax, int hkv,
+                                                    bool aligned) {
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid < hkv) dvmax[gid] = 0;  // for kvprep_kernel, launched next
     if (gid >= (int64_t)n_q * H * kBlocksPerHead) return;
     const int b = (int)(gid % kBlocksPerHead);
     const int64_t row = gid / kBlocksPerHead;  // t * H + h
@@ -225,11 +232,18 @@ __global__ __launch_bounds__(256) void qprep_kernel(const char *__restrict__ q, 
     const float *x = reinterpret_cast<const float *>(q + t * nb1 + h * nb2) + 32 * b;
     float v[32];
     float amax = 0.0f;
+    if (aligned) {  // 16-byte aligned rows: vector loads
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-        v[j] = x[j];
-        amax = fmaxf(amax, fabsf(v[j]));
+        for (int j = 0; j < 8; ++j) {
+            const float4 f = reinterpret_cast<const float4 *>(x)[j];
+            v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; ++j) v[j] = x[j];
     }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
     const float d = amax / 127.f;
     const float id = amax != 0.0f ? 127.f / amax : 0.0f;
     uint16_t oc[32];
@@ -442,7 +456,6 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             issue(t + 1 < n_tiles ? t + 1 : -1, t < n_tiles ? t : -1);
             if (t == n_tiles) break;
             const int64_t kt = k_begin + (int64_t)t * kPK;
-            const uint8_t *ks = smem + (t & 1) * kKStage;
             const int nvalid = (int)(k_end - kt < kPK ? k_end - kt : kPK);
             // this tile's four per-lane K bases, opaque to the compiler: every K read
             // is then one of them plus an immediate offset (hoisting all 64
@@ -739,14 +752,13 @@ int launch_fa_prefill(const FaArgs &a, hipStream_t s) {
 
     int prof = profile_start("fa_prefill_prep", s);
     {
-        const int64_t nk = pl.kv_tiles * kPK * Hkv * kBlocksPerHead;
-        kdeq_kernel<<<dim3((unsigned)((nk + 255) / 256)), dim3(256), 0, s>>>(
-            (const uint8_t *)k.data, (int64_t)k.nb[1], (int64_t)k.nb[2], n_kv, pl.kv_tiles, (int)Hkv, kv, dvmax);
-        vdeq_kernel<<<dim3((unsigned)(pl.kv_tiles / 2), (unsigned)Hkv), dim3(256), 0, s>>>(
-            (const uint8_t *)v.data, (int64_t)v.nb[1], (int64_t)v.nb[2], n_kv, pl.kv_tiles, kv, dvmax);
         const int64_t nqb = n_q * H * kBlocksPerHead;
         qprep_kernel<<<dim3((unsigned)((nqb + 255) / 256)), dim3(256), 0, s>>>(
-            (const char *)q.data, (int64_t)q.nb[1], (int64_t)q.nb[2], (int)n_q, (int)H, a.scale * kLog2e, qc, qd);
+            (const char *)q.data, (int64_t)q.nb[1], (int64_t)q.nb[2], (int)n_q, (int)H, a.scale * kLog2e, qc, qd,
+            dvmax, (int)Hkv, (uintptr_t)q.data % 16 == 0 && q.nb[1] % 16 == 0 && q.nb[2] % 16 == 0);
+        kvprep_kernel<<<dim3((unsigned)(pl.kv_tiles / 2), (unsigned)Hkv), dim3(256), 0, s>>>(
+            (const uint8_t *)k.data, (int64_t)k.nb[1], (int64_t)k.nb[2], (const uint8_t *)v.data, (int64_t)v.nb[1],
+            (int64_t)v.nb[2], n_kv, pl.kv_tiles, kv, dvmax);
         if (mask_src) {
             int64_t grid = (p.mask_len * n_q + 255) / 256;
             if (grid > 2048) grid = 2048;

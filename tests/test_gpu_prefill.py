@@ -79,3 +79,14 @@ def test_rising_logits_force_rescales(sqa, orc, dev, n_q):
     err = rel_err(got, ref)
     print(f"rising logits n_q={n_q}: max err / rms = {err:.3e}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("H,Hkv,n_q", [(4, 2, 6), (4, 1, 1), (8, 4, 3), (16, 2, 5)])
+def test_small_chunks_outside_the_decode_kernel(sqa, orc, dev, H, Hkv, n_q):
+    """Shapes the split-KV decode kernel does not take (more than 4 positions,
+    or n_head_kv != 2) run as prefill chunks, whatever their row count."""
+    q, kq, vq = qkv(orc, 31 + n_q, n_q, 700, H=H, Hkv=Hkv)
+    mask = orc.causal_mask(n_q, 700, 700 - n_q)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    assert rel_err(got, ref) <= TOL
