@@ -113,6 +113,8 @@ __device__ __forceinline__ void wait_vm_barrier(int n) {
     }
 }
 
+typedef const __attribute__((address_space(3))) uint32_t lds_u32;  // LDS dword from a raw LDS address
+
 __device__ __forceinline__ uint32_t lds32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
 __device__ __forceinline__ uint32_t lds16(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
 
@@ -505,15 +507,32 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // Q rows read
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // Q operands published
         const int dq = wq;  // dims 64dq..64dq+63: blocks 2dq, 2dq+1
-        uint32_t magic;     // fp16 0x6400 = 1024 in both halves; in a VGPR so v_and_or_b32 takes it
-        asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
-        const half2v off8 = {(_Float16)-1032.0f, (_Float16)-1032.0f};  // 1024 + 8
+        // Nibble -> exact fp16 integer: the low nibble in mantissa bits 0-3 under
+        // exponent 10 is 1024 + lo; the high nibble left in bits 4-7 under exponent
+        // 6 is 64 + hi. Both constants sit in VGPRs so v_and_or_b32 takes them.
+        uint32_t magic_lo, magic_hi;
+        asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic_lo));
+        asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(magic_hi));
+        const half2v off_lo = {(_Float16)-1032.0f, (_Float16)-1032.0f};  // 1024 + 8
+        const half2v off_hi = {(_Float16)-72.0f, (_Float16)-72.0f};      // 64 + 8
         uint8_t *dv_comp = smem + kOffDv + (wave - kScoreWaves) * 256;  // [bl][half][g][j] fp16
         const int ra = n & kRowMask;  // P row of this lane's A operand
         // d_v compaction: lane -> block bl, half h, key group gg, pair jj: keys 32h + 8jj + gg (+4)
         const int cbl = lane >> 5, ch = (lane >> 4) & 1, cgg = (lane >> 2) & 3, cjj = lane & 3;
         const int ckey = 32 * ch + 8 * cjj + cgg;
         const int cdst = ((cbl * 2 + ch) * 4 + cgg) * 16 + 4 * cjj;  // bytes
+        const uint32_t csrc = (uint32_t)(ckey * kLdsRow + kvh * kHeadRowBytes + 18 * (2 * dq + cbl));
+        // V bytes of this lane: byte n of block 2dq + bl's qs for key 32h + 4j + g
+        // sits at row (32h + 4j + g), column c = kvh*144 + 2 + 18*(2dq + bl) + n: the
+        // dword at c & ~3 holds it as byte c & 3 (= (2 + n) & 3 for bl 0, n & 3 for bl 1).
+        const uint32_t vlane0 = (uint32_t)(g * kLdsRow + kvh * kHeadRowBytes + ((2 + 36 * dq + n) & ~3));
+        const uint32_t vlane1 = (uint32_t)(g * kLdsRow + kvh * kHeadRowBytes + ((20 + 36 * dq + n) & ~3));
+        uint32_t vsel[2];  // v_perm selector: byte c&3 of the lower key's dword -> bits 0-7, of the upper -> 16-23
+#pragma unroll
+        for (int bl = 0; bl < 2; ++bl) {
+            const uint32_t b = (uint32_t)((2 + 18 * bl + n) & 3);
+            vsel[bl] = b | (0x0cu << 8) | ((4u + b) << 16) | (0x0cu << 24);
+        }
 
         floatx4 acc[4];  // O[row 4g+i][dim 64dq + 16T + n]; T = 2*bl + (high nibble)
 #pragma unroll
@@ -529,11 +548,32 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             const int tv = t - 1;  // PV of the tile whose P the score wavefronts wrote last
             const int pb = tv & 1;
             const int64_t kt = k0 + (int64_t)tv * kTileKeys;
-            const uint8_t *sV = smem + kOffV + (tv % kVStages) * kTensorBytes + kvh * kHeadRowBytes;
+            const uint32_t sv_off = (uint32_t)(kOffV + (tv % kVStages) * kTensorBytes);  // wave-uniform
+
+            // -- the slice's V bytes for all 64 keys: 16 registers, two keys each ---
+            // x[4*(2h + bl) + m] holds key 32h + 8m + g (bits 0-7) and key 32h + 8m + 4 + g
+            // (bits 16-23), byte n of block 2dq + bl's qs.
+            uint32_t x[16];
+            {
+                // one base register per block, immediate row offsets (kept opaque so
+                // the loop does not grow one induction variable per address)
+                uint32_t vaddr0 = lds0 + sv_off + vlane0, vaddr1 = lds0 + sv_off + vlane1;
+                asm volatile("" : "+v"(vaddr0), "+v"(vaddr1));
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int bl = 0; bl < 2; ++bl)
+#pragma unroll
+                        for (int m = 0; m < 4; ++m) {
+                            const lds_u32 *r0 = reinterpret_cast<const lds_u32 *>((uintptr_t)(bl ? vaddr1 : vaddr0)) +
+                                                (32 * h + 8 * m) * (kLdsRow / 4);
+                            x[4 * (2 * h + bl) + m] = __builtin_amdgcn_perm(r0[kLdsRow], r0[0], vsel[bl]);
+                        }
+            }
 
             // -- d_v of the slice's two blocks for all 64 keys, in B k-slot order --
             {
-                const uint8_t *src = sV + ckey * kLdsRow + 18 * (2 * dq + cbl);
+                const uint8_t *src = smem + sv_off + csrc;
                 uint32_t da = lds16(src), db = lds16(src + 4 * kLdsRow);
                 if (kt + kTileKeys > k1) {  // rows past the range may hold any bytes: zero scales keep P*V finite
                     da = kt + ckey < k1 ? da : 0u;
@@ -572,38 +612,31 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                 for (int h = 0; h < 2; ++h)
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        const float x = ((float)pa[h][e] + (float)pl[h][e]) * exp2_or_zero(mw[2 * h + (e >> 2)], mna);
-                        pa[h][e] = (_Float16)x;
-                        pl[h][e] = (_Float16)(x - (float)pa[h][e]);
+                        const float xv = ((float)pa[h][e] + (float)pl[h][e]) * exp2_or_zero(mw[2 * h + (e >> 2)], mna);
+                        pa[h][e] = (_Float16)xv;
+                        pl[h][e] = (_Float16)(xv - (float)pa[h][e]);
                     }
             }
 
             // -- O += P V over the two halves of the tile and the slice's blocks ---
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                // B k-slot 8g + j is key 32h + 4j + g: byte n of the block's qs
-                const uint8_t *vr = sV + (32 * h + g) * kLdsRow + 2 + n;
 #pragma unroll
                 for (int bl = 0; bl < 2; ++bl) {
-                    const int b = 2 * dq + bl;
-                    const uint8_t *vb = vr + 18 * b;
-                    uint32_t x[4];
-#pragma unroll
-                    for (int m = 0; m < 4; ++m)
-                        x[m] = (uint32_t)vb[8 * m * kLdsRow] | ((uint32_t)vb[(8 * m + 4) * kLdsRow] << 16);
                     const uint4 dv4 = *reinterpret_cast<const uint4 *>(dv_comp + ((bl * 2 + h) * 4 + g) * 16);
                     const uint32_t dvw[4] = {dv4.x, dv4.y, dv4.z, dv4.w};
                     half8 blo, bhi;
 #pragma unroll
                     for (int m = 0; m < 4; ++m) {
-                        const uint32_t lw = (x[m] & 0x000F000Fu) | magic;
-                        const uint32_t hw = ((x[m] >> 4) & 0x000F000Fu) | magic;
+                        const uint32_t xm = x[4 * (2 * h + bl) + m];
+                        const uint32_t lw = (xm & 0x000F000Fu) | magic_lo;
+                        const uint32_t hw = (xm & 0x00F000F0u) | magic_hi;
                         half2v lo, hi, dv2;
                         __builtin_memcpy(&lo, &lw, 4);
                         __builtin_memcpy(&hi, &hw, 4);
                         __builtin_memcpy(&dv2, &dvw[m], 4);
-                        lo = (lo + off8) * dv2;  // (nib - 8) * d_v
-                        hi = (hi + off8) * dv2;
+                        lo = (lo + off_lo) * dv2;  // (nib - 8) * d_v
+                        hi = (hi + off_hi) * dv2;
                         blo[2 * m] = lo[0];
                         blo[2 * m + 1] = lo[1];
                         bhi[2 * m] = hi[0];
