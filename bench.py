@@ -216,7 +216,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # ~10 ms of untimed decode steps: the GPU reaches its steady clock after a few
+    # ms of load, and a decode server runs continuously.
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-verify", action="store_true", help="skip the n_q=2 verify leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the pp512 prefill leg")

@@ -93,16 +93,23 @@ static_assert(32 * 1024 <= (kVStages - 1) * kTensorBytes, "Q staging must fit in
 
 // 16 bytes per lane from sbase + voff into LDS at m0 + 16 * lane. The data
 // arrives asynchronously; the caller waits with s_waitcnt vmcnt.
+// sbase and m0v are wave-uniform; readfirstlane keeps them in SGPRs even where
+// the compiler has placed them in VGPRs.
 __device__ __forceinline__ void dma16(uint32_t voff, const void *sbase, uint32_t m0v) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0v)
-                 : "memory");
+    const uint64_t b = (uint64_t)(uintptr_t)sbase;
+    const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(b >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    const uint32_t ms = (uint32_t)__builtin_amdgcn_readfirstlane((int)m0v);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(bs), "s"(ms) : "memory");
 }
 
 // Wait until at most n vector-memory loads of this wavefront are outstanding
 // and its LDS accesses are done, then synchronise the workgroup. n is
 // wave-uniform and small.
 __device__ __forceinline__ void wait_vm_barrier(int n) {
-    switch (n) {
+    // a switch on a value the compiler deems divergent would run several cases,
+    // i.e. several barriers, under partial exec masks: force it scalar
+    switch (__builtin_amdgcn_readfirstlane(n)) {
 #define SQA_WAIT_CASE(N) \
     case N: asm volatile("s_waitcnt vmcnt(" #N ") lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
         SQA_WAIT_CASE(0) SQA_WAIT_CASE(1) SQA_WAIT_CASE(2) SQA_WAIT_CASE(3) SQA_WAIT_CASE(4)
@@ -286,7 +293,9 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
         float l_acc = 0.0f;        // this lane's share of the row's sum, relative to m_ref
         float l_prev = 0.0f;       // the last tile's share, relative to m_used
 
-        for (int t = 0; t <= n_tiles; ++t) {
+        for (int tt = 0; tt <= n_tiles; ++tt) {
+            // the tile index is wave-uniform; with 16 rows the compiler loses track of that
+            const int t = TWO ? __builtin_amdgcn_readfirstlane(tt) : tt;
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // K(t) and P(t-1) readable
 
             // -- fold the last tile's sum into l under the KV head's common max --
@@ -539,7 +548,8 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
         for (int T = 0; T < 4; ++T) acc[T] = floatx4{0.f, 0.f, 0.f, 0.f};
         float m_acc[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // reference max of rows 4g+i
 
-        for (int t = 0; t <= n_tiles; ++t) {
+        for (int tt = 0; tt <= n_tiles; ++tt) {
+            const int t = TWO ? __builtin_amdgcn_readfirstlane(tt) : tt;  // wave-uniform tile index
             wait_vm_barrier(younger_than_needed(t));
             if (t + kKStages - 1 < n_tiles) issue_k(t + kKStages - 1);
             if (t + 1 < n_tiles) issue_v(t + 1, (t + 1) % kVStages);
