@@ -370,10 +370,10 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                 if (TWO) {  // lanes n < 8 take rows 0-7 (set 0), lanes n >= 8 rows 8-15 (set 1)
                     const float u = n < 8 ? xs[0][i] : xs[1][i];
                     const float w = n < 8 ? xs[1][i] : xs[0][i];
-                    s[i] = u + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(w), 0x128, 0xf, 0xf, false));
+                    s[i] = u + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(w), 0x128, 0xf, 0xf, true));
                 } else {
                     s[i] = xs[0][i] +
-                           __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(xs[0][i]), 0x128, 0xf, 0xf, false));
+                           __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(xs[0][i]), 0x128, 0xf, 0xf, true));
                 }
             }
             // mask (F16, base-e units) and the ragged / causal tail
@@ -416,11 +416,18 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             const int buf = t & 1;
             if (row_writer) {
                 half4 ph, pl;
+                ph = half4{(_Float16)pv[0], (_Float16)pv[1], (_Float16)pv[2], (_Float16)pv[3]};
+                uint32_t hw[2];
+                __builtin_memcpy(hw, &ph, 8);
+                float r[4];  // exact residual p - hi, read from the packed fp16 halves by v_fma_mix
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    ph[i] = (_Float16)pv[i];
-                    pl[i] = (_Float16)(pv[i] - (float)ph[i]);
+                    if (i & 1)
+                        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "=v"(r[i]) : "v"(pv[i]), "v"(hw[i >> 1]));
+                    else
+                        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[0,0,0] op_sel_hi:[0,0,1]" : "=v"(r[i]) : "v"(pv[i]), "v"(hw[i >> 1]));
                 }
+                pl = half4{(_Float16)r[0], (_Float16)r[1], (_Float16)r[2], (_Float16)r[3]};
                 _Float16 *prow = pbuf + ((buf * 2 + kvh) * 16 + my_r) * kPRow + p_col;
                 *reinterpret_cast<half4 *>(prow) = ph;
                 *reinterpret_cast<half4 *>(prow + 64) = pl;
