@@ -154,6 +154,25 @@ __device__ __forceinline__ uint32_t tile_slot_offset(int j, int lane) {
     return (uint32_t)(row * kRowBytes + (col < 17 ? col : 17) * 16);
 }
 
+// V tiles land rotated: row r's 16-byte chunks start 2*((r >> 3) & 3) slots later
+// (mod 19), so the four 8-row key groups that a value wavefront reads together
+// sit on disjoint banks.
+__device__ __forceinline__ int v_rot(int row) { return 2 * ((row >> 3) & 3); }
+__device__ __forceinline__ uint32_t v_slot_offset(int j, int lane) {
+    const int s = 64 * j + lane;
+    const int row = s / kSlotsPerRow;
+    const int slot = s - row * kSlotsPerRow;
+    int c = slot - v_rot(row);
+    c = c < 0 ? c + kSlotsPerRow : c;
+    return (uint32_t)(row * kRowBytes + (c < 17 ? c : 17) * 16);
+}
+// LDS byte of cache-row byte c (0..287) of V row `row` inside a tile stage
+__device__ __forceinline__ int v_lds_byte(int row, int c) {
+    int slot = (c >> 4) + v_rot(row);
+    slot = slot >= kSlotsPerRow ? slot - kSlotsPerRow : slot;
+    return row * kLdsRow + slot * 16 + (c & 15);
+}
+
 // TWO = false: up to 8 query rows per KV head (one block-diagonal B set).
 // TWO = true : 9..16 rows (rows 0-7 and 8-15 as two B sets, one A operand).
 template <bool TWO>
@@ -284,9 +303,8 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
         const uint32_t ka_shift = (ka_blk_par ? 0u : 16u) + 4u * (uint32_t)(g & 1);
         uint8_t *dk_comp = smem + kOffDk + wave * 256;  // [8 blocks][16 keys] fp16
         const int key0 = 16 * wq;                       // first key of this wavefront in a tile
-        // P slot of this lane's four keys: key key0 + g + 4i is k-slot 8g + 4(wq & 1) + i
-        // of the PV half-tile wq >> 1 (the value wavefronts' B row order).
-        const int p_col = 32 * (wq >> 1) + 8 * g + 4 * (wq & 1);
+        // P is stored in key order: this lane's four keys key0 + 4g + i
+        const int p_col = key0 + 4 * g;
 
         float m_ref = -INFINITY;   // base-2 reference max of row my_r (common to the KV head)
         float m_used = -INFINITY;  // reference this wavefront used for the last tile's P
@@ -319,23 +337,22 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             // a tile holding keys past the range end or past a causal limit
             const bool tail = kt + kTileKeys > k1 || (p.q_pos0 >= 0 && kt + kTileKeys - 1 > p.q_pos0);
 
-            // The wavefront's 16 keys enter the QK A operand permuted: row r is key
-            // key0 + (r >> 2) + 4*(r & 3), so lane group g holds keys key0 + g + 4i.
+            // A row r of QK is key key0 + r, so lane group g holds keys key0 + 4g + i.
             // -- compact d_k of those keys, [block][4g + i] ------------------------
             {
                 const int blk = lane >> 3, gg = lane & 3, hh = (lane >> 2) & 1;
-                const uint8_t *src = sK + (key0 + gg + 8 * hh) * kLdsRow + 18 * blk;
+                const uint8_t *src = sK + (key0 + 4 * gg + 2 * hh) * kLdsRow + 18 * blk;
                 *reinterpret_cast<uint32_t *>(dk_comp + (blk * 16 + 4 * gg + 2 * hh) * 2) =
-                    lds16(src) | (lds16(src + 4 * kLdsRow) << 16);
+                    lds16(src) | (lds16(src + kLdsRow) << 16);
             }
 
-            // -- QK: xs[i] = S[key key0+g+4i][row of column n] --------------------
+            // -- QK: xs[i] = S[key key0+4g+i][row of column n] --------------------
             float xs[kSets][4];
 #pragma unroll
             for (int set = 0; set < kSets; ++set)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) xs[set][i] = 0.0f;
-            const uint8_t *krow = sK + (key0 + (n >> 2) + 4 * (n & 3)) * kLdsRow;
+            const uint8_t *krow = sK + (key0 + n) * kLdsRow;
 #pragma unroll
             for (int pr = 0; pr < 4; ++pr) {
                 // key of A row n, block 2*pair + (g >> 1): five dwords from the aligned
@@ -351,7 +368,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                 int32x4 aop;
                 __builtin_memcpy(&aop, aw, 16);
                 const uint2 dk2 = *reinterpret_cast<const uint2 *>(dk_comp + ((2 * pr + (n >> 3)) * 16 + 4 * g) * 2);
-                half4 dkh;  // d_k of keys key0+g+4i, block of column n
+                half4 dkh;  // d_k of keys key0+4g+i, block of column n
                 __builtin_memcpy(&dkh, &dk2, 8);
 #pragma unroll
                 for (int set = 0; set < kSets; ++set) {
@@ -379,10 +396,10 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             // mask (F16, base-e units) and the ragged / causal tail
             if (p.mask) {
                 const uint16_t *mrow = reinterpret_cast<const uint16_t *>(smem + kOffMask + st * kMaskStageBytes) +
-                                       my_t * kTileKeys + key0 + g;
+                                       my_t * kTileKeys + key0 + 4 * g;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const uint16_t mb = mrow[4 * i];
+                    const uint16_t mb = mrow[i];
                     _Float16 mh;
                     __builtin_memcpy(&mh, &mb, 2);
                     s[i] = fmaf((float)mh, kLog2e, s[i]);
@@ -391,7 +408,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             if (tail) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int64_t key = kt + key0 + g + 4 * i;
+                    const int64_t key = kt + key0 + 4 * g + i;
                     bool dead = key >= k1;
                     if (p.q_pos0 >= 0) dead = dead || key > p.q_pos0 + my_t;
                     s[i] = dead ? -INFINITY : s[i];
@@ -463,7 +480,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             const int jk = vw + 8 * r;
             const int jv = ((vw + 5) & 7) + 8 * r;
             koff[r] = tile_slot_offset(jk < kTensorInsts ? jk : 0, lane);
-            voff[r] = tile_slot_offset(jv < kTensorInsts ? jv : 0, lane);
+            voff[r] = v_slot_offset(jv < kTensorInsts ? jv : 0, lane);
             nk += jk < kTensorInsts;
             nv += jv < kTensorInsts;
         }
@@ -533,20 +550,22 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
         const half2v off_hi = {(_Float16)-72.0f, (_Float16)-72.0f};      // 64 + 8
         uint8_t *dv_comp = smem + kOffDv + (wave - kScoreWaves) * 256;  // [bl][half][g][j] fp16
         const int ra = n & kRowMask;  // P row of this lane's A operand
-        // d_v compaction: lane -> block bl, half h, key group gg, pair jj: keys 32h + 8jj + gg (+4)
+        // d_v compaction: lane -> block bl, half h, key group gg, pair jj: keys
+        // 32h + 8gg + 2jj and the next one (B k-slots 8gg + 2jj, +1)
         const int cbl = lane >> 5, ch = (lane >> 4) & 1, cgg = (lane >> 2) & 3, cjj = lane & 3;
-        const int ckey = 32 * ch + 8 * cjj + cgg;
+        const int ckey = 32 * ch + 8 * cgg + 2 * cjj;
         const int cdst = ((cbl * 2 + ch) * 4 + cgg) * 16 + 4 * cjj;  // bytes
-        const uint32_t csrc = (uint32_t)(ckey * kLdsRow + kvh * kHeadRowBytes + 18 * (2 * dq + cbl));
-        // V bytes of this lane: byte n of block 2dq + bl's qs for key 32h + 4j + g
-        // sits at row (32h + 4j + g), column c = kvh*144 + 2 + 18*(2dq + bl) + n: the
-        // dword at c & ~3 holds it as byte c & 3 (= (2 + n) & 3 for bl 0, n & 3 for bl 1).
-        const uint32_t vlane0 = (uint32_t)(g * kLdsRow + kvh * kHeadRowBytes + ((2 + 36 * dq + n) & ~3));
-        const uint32_t vlane1 = (uint32_t)(g * kLdsRow + kvh * kHeadRowBytes + ((20 + 36 * dq + n) & ~3));
-        uint32_t vsel[2];  // v_perm selector: byte c&3 of the lower key's dword -> bits 0-7, of the upper -> 16-23
+        const uint32_t csrc = (uint32_t)v_lds_byte(ckey, kvh * kHeadRowBytes + 18 * (2 * dq + cbl));
+        // V bytes of this lane: B k-slot 8g + j is key 32h + 8g + j; its byte n of block
+        // 2dq + bl sits at column c = kvh*144 + 2 + 18*(2dq + bl) + n of the row, rotated
+        // by v_rot = 2g chunks for every row the lane reads; the dword holding it carries
+        // it as byte c & 3.
+        uint32_t vlane[2], vsel[2];  // v_perm selector: byte c&3 of the lower key's dword -> bits 0-7, of the upper -> 16-23
 #pragma unroll
         for (int bl = 0; bl < 2; ++bl) {
-            const uint32_t b = (uint32_t)((2 + 18 * bl + n) & 3);
+            const int c = kvh * kHeadRowBytes + 2 + 18 * (2 * dq + bl) + n;
+            vlane[bl] = (uint32_t)(v_lds_byte(8 * g, c) & ~3);
+            const uint32_t b = (uint32_t)(c & 3);
             vsel[bl] = b | (0x0cu << 8) | ((4u + b) << 16) | (0x0cu << 24);
         }
 
@@ -568,33 +587,34 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             const uint32_t sv_off = (uint32_t)(kOffV + (tv % kVStages) * kTensorBytes);  // wave-uniform
 
             // -- the slice's V bytes for all 64 keys: 16 registers, two keys each ---
-            // x[4*(2h + bl) + m] holds key 32h + 8m + g (bits 0-7) and key 32h + 8m + 4 + g
-            // (bits 16-23), byte n of block 2dq + bl's qs.
+            // x[4*(2h + bl) + m] holds keys 32h + 8g + 2m (bits 0-7) and 32h + 8g + 2m + 1
+            // (bits 16-23), byte n of block 2dq + bl's qs: adjacent rows, one ds_read2_b32
+            // each. A base per two pairs keeps both dword offsets within ds_read2's 8 bits.
             uint32_t x[16];
-            {
-                // one base register per block, immediate row offsets (kept opaque so
-                // the loop does not grow one induction variable per address)
-                uint32_t vaddr0 = lds0 + sv_off + vlane0, vaddr1 = lds0 + sv_off + vlane1;
-                asm volatile("" : "+v"(vaddr0), "+v"(vaddr1));
+#pragma unroll
+            for (int bl = 0; bl < 2; ++bl)
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
 #pragma unroll
-                    for (int bl = 0; bl < 2; ++bl)
+                    for (int mp = 0; mp < 2; ++mp) {
+                        uint32_t va = lds0 + sv_off + vlane[bl] + (uint32_t)((32 * h + 4 * mp) * kLdsRow);
+                        asm volatile("" : "+v"(va));  // opaque: no induction variable per address
+                        const lds_u32 *r0 = reinterpret_cast<const lds_u32 *>((uintptr_t)va);
 #pragma unroll
-                        for (int m = 0; m < 4; ++m) {
-                            const lds_u32 *r0 = reinterpret_cast<const lds_u32 *>((uintptr_t)(bl ? vaddr1 : vaddr0)) +
-                                                (32 * h + 8 * m) * (kLdsRow / 4);
-                            x[4 * (2 * h + bl) + m] = __builtin_amdgcn_perm(r0[kLdsRow], r0[0], vsel[bl]);
+                        for (int m2 = 0; m2 < 2; ++m2) {
+                            const int m = 2 * mp + m2;
+                            x[4 * (2 * h + bl) + m] = __builtin_amdgcn_perm(r0[(2 * m2 + 1) * (kLdsRow / 4)],
+                                                                            r0[2 * m2 * (kLdsRow / 4)], vsel[bl]);
                         }
-            }
+                    }
 
             // -- d_v of the slice's two blocks for all 64 keys, in B k-slot order --
             {
                 const uint8_t *src = smem + sv_off + csrc;
-                uint32_t da = lds16(src), db = lds16(src + 4 * kLdsRow);
+                uint32_t da = lds16(src), db = lds16(src + kLdsRow);
                 if (kt + kTileKeys > k1) {  // rows past the range may hold any bytes: zero scales keep P*V finite
                     da = kt + ckey < k1 ? da : 0u;
-                    db = kt + ckey + 4 < k1 ? db : 0u;
+                    db = kt + ckey + 1 < k1 ? db : 0u;
                 }
                 *reinterpret_cast<uint32_t *>(dv_comp + cdst) = da | (db << 16);
             }
@@ -620,7 +640,8 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                 const floatx4 f4 = {fac[0], fac[1], fac[2], fac[3]};
 #pragma unroll
                 for (int T = 0; T < 4; ++T) acc[T] *= f4;
-                // P of score wavefront w (k-slots 8g + 4(w & 1) .. of half w >> 1) onto the new max
+                // P of score wavefront w (keys 16w..16w+15: this lane's half-h slots 8g..8g+7
+                // come from wavefront 2h + (g >> 1)) onto the new max
                 float mw[4];
 #pragma unroll
                 for (int w = 0; w < 4; ++w) mw[w] = mr[16 * w + ra];
@@ -629,7 +650,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                 for (int h = 0; h < 2; ++h)
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        const float xv = ((float)pa[h][e] + (float)pl[h][e]) * exp2_or_zero(mw[2 * h + (e >> 2)], mna);
+                        const float xv = ((float)pa[h][e] + (float)pl[h][e]) * exp2_or_zero(mw[2 * h + (g >> 1)], mna);
                         pa[h][e] = (_Float16)xv;
                         pl[h][e] = (_Float16)(xv - (float)pa[h][e]);
                     }
