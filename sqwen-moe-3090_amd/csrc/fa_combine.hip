@@ -75,6 +75,70 @@ __global__ __launch_bounds__(256) void fa_combine_kernel(const float *__restrict
     }
 }
 
+// The same merge for up to 256 splits with one memory latency on the path: each
+// thread issues the loads of its 16 splits' acc values and (m, l) pairs at once,
+// then the maximum, the weights and the sums follow from registers, with
+// cross-lane reductions inside a wavefront and one LDS exchange per quantity
+// across the 4 wavefronts. Grid and thread roles as in fa_combine_kernel.
+constexpr int kFastSplits = 256;
+__global__ __launch_bounds__(256) void fa_combine_fast_kernel(const float *__restrict__ part_acc,
+                                                              const float *__restrict__ part_ml,
+                                                              int n_splits, int rows_total,
+                                                              float *__restrict__ dst, const char *gate,
+                                                              int64_t gate_nb1, int64_t gate_nb2, int H) {
+    __shared__ float xm[4], xo[4][16], xl[4];
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int dl = tid & 15, sg = tid >> 4, wv = tid >> 6;
+    const int d = blockIdx.y * 16 + dl;
+    const int64_t sstride = (int64_t)rows_total * 256;
+    const float *pa = part_acc + (int64_t)row * 256 + d;
+    const float2 *pm = reinterpret_cast<const float2 *>(part_ml) + row;
+    float acc[16];
+    float2 ml[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int sp = sg + 16 * j;
+        const bool ok = sp < n_splits;
+        acc[j] = ok ? pa[sp * sstride] : 0.0f;
+        ml[j] = ok ? pm[(int64_t)sp * rows_total] : make_float2(-INFINITY, 0.0f);
+    }
+    // M: maximum over all splits (lanes 16 apart hold other split groups)
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) m = fmaxf(m, ml[j].x);
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    if ((tid & 63) == 0) xm[wv] = m;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(xm[0], xm[1]), fmaxf(xm[2], xm[3]));
+    float o = 0.0f, l = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const float w = (M == -INFINITY || ml[j].x == -INFINITY) ? 0.0f : exp2f((ml[j].x - M) * kLog2e);
+        o = fmaf(acc[j], w, o);
+        l = fmaf(ml[j].y, w, l);
+    }
+    o += __shfl_xor(o, 16);
+    o += __shfl_xor(o, 32);
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if ((tid & 63) < 16) xo[wv][dl] = o;
+    if ((tid & 63) == 0) xl[wv] = l;
+    __syncthreads();
+    if (tid < 16) {
+        const float ot = (xo[0][dl] + xo[1][dl]) + (xo[2][dl] + xo[3][dl]);
+        const float L = (xl[0] + xl[1]) + (xl[2] + xl[3]);
+        float r = (L == 0.0f) ? 0.0f : ot * (1.0f / L);
+        if (gate) {
+            const int t = row / H, h = row % H;
+            const float gv = reinterpret_cast<const float *>(gate + t * gate_nb2 + h * gate_nb1)[d];
+            r = r * (1.0f / (1.0f + expf(-gv)));
+        }
+        dst[(int64_t)row * 256 + d] = r;
+    }
+}
+
 // The same merge for many rows and few splits (prefill): 64 threads per row,
 // one float4 of the row each, 4 rows per block; every thread walks the splits
 // itself (the (m, l) pairs are the same for the 64 threads of a row and come
@@ -130,6 +194,9 @@ int launch_fa_combine(const float *part_acc, const float *part_ml, int n_splits,
     const int prof = profile_start("fa_combine", s);
     if (n_splits <= kRowsMaxSplits && rows_total >= 64) {
         fa_combine_rows_kernel<<<dim3((unsigned)((rows_total + 3) / 4)), dim3(256), 0, s>>>(
+            part_acc, part_ml, n_splits, rows_total, dst, g, g1, g2, H);
+    } else if (n_splits <= kFastSplits) {
+        fa_combine_fast_kernel<<<dim3((unsigned)rows_total, 16), dim3(256), 0, s>>>(
             part_acc, part_ml, n_splits, rows_total, dst, g, g1, g2, H);
     } else {
         fa_combine_kernel<<<dim3((unsigned)rows_total, 16), dim3(256), 0, s>>>(part_acc, part_ml, n_splits,
