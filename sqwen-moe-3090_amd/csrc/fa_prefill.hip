@@ -95,6 +95,17 @@ __device__ __forceinline__ uint4 swap_halves(uint4 v, bool swap) {
     return swap ? make_uint4(v.z, v.w, v.x, v.y) : v;
 }
 
+// max(x, x of lane ^ 16) and max(x, x of lane ^ 32) with gfx950's row swaps (no
+// LDS round trip): each swap returns the two halves of a lane pair's values.
+__device__ __forceinline__ float xmax16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xmax32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // LDS/record row of key k (0..31) of a tile: the inverse of sigma.
 __device__ __forceinline__ int key_row(int k) { return 16 * ((k >> 2) & 1) + 4 * (k >> 3) + (k & 3); }
 
@@ -468,6 +479,13 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                     kb[bp][hf] = (t & 1) * kKStage + k_off[bp][hf];
                     asm volatile("" : "+v"(kb[bp][hf]));
                 }
+            // mask rows of the tile, read now so that their latency hides behind QK
+            uint4 mrow[kRG];
+            if (p.mask) {
+#pragma unroll
+                for (int rg = 0; rg < kRG; ++rg)
+                    mrow[rg] = *reinterpret_cast<const uint4 *>(smem + m_off[rg] + (t & 1) * p.mask_stage);
+            }
             // ---- S^T: sa[rg][kg][i] = S[key kt + 8g + 4kg + i][row n of group rg] ----
             floatx4 sa[kRG][2];
 #pragma unroll
@@ -497,8 +515,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             if (p.mask) {
 #pragma unroll
                 for (int rg = 0; rg < kRG; ++rg) {
-                    const uint4 mr = *reinterpret_cast<const uint4 *>(smem + m_off[rg] + (t & 1) * p.mask_stage);
-                    const uint32_t mw[4] = {mr.x, mr.y, mr.z, mr.w};
+                    const uint32_t mw[4] = {mrow[rg].x, mrow[rg].y, mrow[rg].z, mrow[rg].w};
 #pragma unroll
                     for (int jj = 0; jj < 8; ++jj)
                         s[rg][jj] = fmaf(h2f((mw[jj >> 1] >> (16 * (jj & 1))) & 0xffff), kLog2e, s[rg][jj]);
@@ -525,8 +542,8 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                 if (__any(over)) {
                     float mt = fmaxf(fmaxf(fmaxf(s[rg][0], s[rg][1]), fmaxf(s[rg][2], s[rg][3])),
                                      fmaxf(fmaxf(s[rg][4], s[rg][5]), fmaxf(s[rg][6], s[rg][7])));
-                    mt = fmaxf(mt, __shfl_xor(mt, 16));
-                    mt = fmaxf(mt, __shfl_xor(mt, 32));
+                    mt = xmax16(mt);
+                    mt = xmax32(mt);
                     const float m_new = fmaxf(m_run[rg], mt);
                     alpha = m_run[rg] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[rg] - m_new);
                     l_part[rg] *= alpha;
