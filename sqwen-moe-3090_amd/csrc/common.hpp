@@ -42,7 +42,9 @@ struct FaArgs {
     size_t ws_bytes;
 };
 size_t fa_decode_workspace(int64_t n_q, int64_t H, int64_t n_kv);
-// Merges split partials [n_splits][rows][256] + [n_splits][rows][2] into dst.
+// Merges split partials [n_splits][rows][256] + [n_splits][rows][2] into dst;
+// n_splits <= kMaxSplits (the split planners cap there).
+constexpr int kMaxSplits = 256;
 int launch_fa_combine(const float *part_acc, const float *part_ml, int n_splits, int rows_total,
                       float *dst, const sqa_tensor *gate, int H, hipStream_t s);
 int launch_fa_decode(const FaArgs &a, hipStream_t s);

@@ -11,77 +11,14 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// Merge split partials: out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M),
-// optionally times sigmoid(gate). Grid: (rows, 16 chunks of 16 dims); 256
-// threads = 16 dims x 16 split groups, each thread summing every 16th split
-// with all its loads in flight; the split weights are computed once per block.
-constexpr int kMaxSplits = 1024;
+// Merge of up to kMaxSplits (256) split partials with one memory latency on the
+// path. Grid: (rows, 16 chunks of 16 dims); 256 threads = 16 dims x 16 split
+// groups. Each thread issues the loads of its 16 splits' acc values and (m, l)
+// pairs at once; the maximum, the weights and the sums then follow from
+// registers, with cross-lane reductions inside a wavefront and one LDS exchange
+// per quantity across the 4 wavefronts.
+static_assert(kMaxSplits == 256, "16 split groups x 16 splits per thread");
 __global__ __launch_bounds__(256) void fa_combine_kernel(const float *__restrict__ part_acc,
-                                                         const float *__restrict__ part_ml,
-                                                         int n_splits, int rows_total,
-                                                         float *__restrict__ dst, const char *gate,
-                                                         int64_t gate_nb1, int64_t gate_nb2, int H) {
-    __shared__ float wts[kMaxSplits];
-    __shared__ float red[16][17];
-    __shared__ float redm[256];
-    const int row = blockIdx.x;
-    const int tid = threadIdx.x;
-    const int dl = tid & 15;
-    const int sg = tid >> 4;
-    const int d = blockIdx.y * 16 + dl;
-    float mloc = -INFINITY;
-    for (int s = tid; s < n_splits; s += 256) mloc = fmaxf(mloc, part_ml[((int64_t)s * rows_total + row) * 2]);
-    redm[tid] = mloc;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (tid < w) redm[tid] = fmaxf(redm[tid], redm[tid + w]);
-        __syncthreads();
-    }
-    const float M = redm[0];
-    __syncthreads();
-    float lloc = 0.0f;
-    for (int s = tid; s < n_splits; s += 256) {
-        const float ms = part_ml[((int64_t)s * rows_total + row) * 2];
-        const float ls = part_ml[((int64_t)s * rows_total + row) * 2 + 1];
-        const float w = (M == -INFINITY || ms == -INFINITY) ? 0.0f : exp2f((ms - M) * kLog2e);
-        wts[s] = w;
-        lloc += ls * w;
-    }
-    redm[tid] = lloc;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (tid < w) redm[tid] += redm[tid + w];
-        __syncthreads();
-    }
-    const float L = redm[0];
-    const float *pa = part_acc + (int64_t)row * 256 + d;
-    const int64_t sstride = (int64_t)rows_total * 256;
-    float o = 0.0f;
-#pragma unroll 16
-    for (int s = sg; s < n_splits; s += 16) o = fmaf(pa[s * sstride], wts[s], o);
-    red[sg][dl] = o;
-    __syncthreads();
-    if (tid < 16) {
-        float ot = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) ot += red[j][tid];
-        float r = (L == 0.0f) ? 0.0f : ot * (1.0f / L);
-        if (gate) {
-            const int t = row / H, h = row % H;
-            const float gv = reinterpret_cast<const float *>(gate + t * gate_nb2 + h * gate_nb1)[d];
-            r = r * (1.0f / (1.0f + expf(-gv)));
-        }
-        dst[(int64_t)row * 256 + d] = r;
-    }
-}
-
-// The same merge for up to 256 splits with one memory latency on the path: each
-// thread issues the loads of its 16 splits' acc values and (m, l) pairs at once,
-// then the maximum, the weights and the sums follow from registers, with
-// cross-lane reductions inside a wavefront and one LDS exchange per quantity
-// across the 4 wavefronts. Grid and thread roles as in fa_combine_kernel.
-constexpr int kFastSplits = 256;
-__global__ __launch_bounds__(256) void fa_combine_fast_kernel(const float *__restrict__ part_acc,
                                                               const float *__restrict__ part_ml,
                                                               int n_splits, int rows_total,
                                                               float *__restrict__ dst, const char *gate,
@@ -191,12 +128,11 @@ int launch_fa_combine(const float *part_acc, const float *part_ml, int n_splits,
                       float *dst, const sqa_tensor *gate, int H, hipStream_t s) {
     const char *g = gate ? (const char *)gate->data : nullptr;
     const int64_t g1 = gate ? (int64_t)gate->nb[1] : 0, g2 = gate ? (int64_t)gate->nb[2] : 0;
+    if (n_splits > kMaxSplits)
+        return set_error(SQA_ERR_UNSUPPORTED, "fa_combine: %d splits > %d", n_splits, kMaxSplits);
     const int prof = profile_start("fa_combine", s);
     if (n_splits <= kRowsMaxSplits && rows_total >= 64) {
         fa_combine_rows_kernel<<<dim3((unsigned)((rows_total + 3) / 4)), dim3(256), 0, s>>>(
-            part_acc, part_ml, n_splits, rows_total, dst, g, g1, g2, H);
-    } else if (n_splits <= kFastSplits) {
-        fa_combine_fast_kernel<<<dim3((unsigned)rows_total, 16), dim3(256), 0, s>>>(
             part_acc, part_ml, n_splits, rows_total, dst, g, g1, g2, H);
     } else {
         fa_combine_kernel<<<dim3((unsigned)rows_total, 16), dim3(256), 0, s>>>(part_acc, part_ml, n_splits,

@@ -716,7 +716,8 @@ __global__ __launch_bounds__(256) void mask_pack_kernel(const char *__restrict__
 
 int decode_splits(int64_t n_kv) {
     int64_t s = (n_kv + 255) / 256;  // at least ~4 tiles per split
-    const int64_t cap = device_cu_count();
+    int64_t cap = device_cu_count();
+    if (cap > kMaxSplits) cap = kMaxSplits;
     if (s > cap) s = cap;
     if (s < 1) s = 1;
     return (int)s;

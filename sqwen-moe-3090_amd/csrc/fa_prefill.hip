@@ -700,6 +700,7 @@ PrefillPlan plan(int64_t n_q, int64_t H, int64_t Hkv, int64_t n_kv) {
     int64_t splits = (cus + wgs - 1) / wgs;
     const int64_t max_by_len = (n_kv + 511) / 512;  // at least ~512 keys per split
     if (splits > max_by_len) splits = max_by_len;
+    if (splits > kMaxSplits) splits = kMaxSplits;
     if (splits < 1) splits = 1;
     pl.split_len = ((n_kv + splits - 1) / splits + kPK - 1) / kPK * kPK;
     pl.n_splits = (int)((n_kv + pl.split_len - 1) / pl.split_len);
