@@ -34,6 +34,7 @@ extern "C" {
 #define SQA_TYPE_F32 0
 #define SQA_TYPE_F16 1
 #define SQA_TYPE_Q4_0 2
+#define SQA_TYPE_I32 26
 #define SQA_TYPE_I64 27
 
 /* q4_0 block: fp16 scale d + 16 bytes of nibbles, 32 values, 18 bytes
@@ -90,6 +91,50 @@ int sqa_set_rows_q4_0(const sqa_tensor *dst, const sqa_tensor *src, const sqa_te
 /* Support query for set_rows, mirroring ggml_backend_supports_op
  * (reference: src/backend/ffi.rs:361-362). Returns 1 if supported. */
 int sqa_supports_set_rows(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *idx);
+
+/* ------------------------------------------------------------------------ */
+/* K/Q producer: per-head RMSNorm, IMROPE, q4_0 quantize-on-write            */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Rotary parameters of ggml_rope_multi (reference: declaration at
+ * src/backend/ffi.rs:417-432; values from RopeParams, src/model/attn.rs:30-65).
+ * Only the text-mode settings the engine uses are supported: ext_factor must be
+ * 0 (no YaRN ramp, so n_ctx_orig, beta_fast and beta_slow play no part).
+ */
+typedef struct sqa_rope {
+    int32_t n_rot;       /* rotated leading dims of each head row; n_rot % 8 == 0, <= D */
+    int32_t sections[4]; /* IMROPE sections (t, h, w, e), sum > 0 (the engine: n_rot / 2) */
+    float freq_base;
+    float freq_scale;
+    float ext_factor; /* must be 0 */
+    float attn_factor;
+} sqa_rope;
+
+/*
+ * The K producer chain of one full-attention layer in one kernel:
+ *   y = rms_norm(x, eps) * norm_w          (ggml_rms_norm + ggml_mul per head row,
+ *                                           reference: head_rms_norm, src/model/attn.rs:68-84)
+ *   y = rope_multi(y, pos, IMROPE, rope)   (src/model/attn.rs:180-200)
+ *   dst[idx[t], head h] = quantize_row_q4_0(y)   (set_rows of KvCache::append,
+ *                                           src/engine/kv.rs:313-399)
+ *   src    F32  [D, n_head, n_tok] (element stride 4, head stride nb[1], token stride nb[2])
+ *   norm_w F32  [D] contiguous, or NULL for no normalisation (then eps is unused)
+ *   pos    I32  [4 * n_tok] contiguous: t, h, w, e positions (ggml's rope_multi layout)
+ *   idx    I64  [n_tok] destination rows
+ *   dst    Q4_0 [D * n_head, dst_rows] (row stride nb[1]); token t's head h lands at
+ *          blocks h*D/32 .. (h+1)*D/32 - 1 of row idx[t]
+ * D is 64, 128 or 256. Rows whose index lies outside [0, dst_rows) are skipped,
+ * as in sqa_set_rows_q4_0.
+ */
+int sqa_rope_norm_set_rows_q4_0(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w,
+                                float eps, const sqa_tensor *pos, const sqa_rope *rope,
+                                const sqa_tensor *idx, void *stream);
+
+/* The same normalisation and rotation with an F32 result, the Q side of the
+ * layer (src/model/attn.rs:166-199): dst F32 [D, n_head, n_tok] contiguous. */
+int sqa_rope_norm_f32(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w, float eps,
+                      const sqa_tensor *pos, const sqa_rope *rope, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* flash_attn_ext                                                            */

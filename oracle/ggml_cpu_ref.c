@@ -346,6 +346,130 @@ int orc_sigmoid_mul(const sqa_tensor *dst, const sqa_tensor *x, const sqa_tensor
     return SQA_OK;
 }
 
+/* -------------------------------------------- K/Q producer: norm + rope --- */
+
+/* ggml_rms_norm (CPU): the squares summed in double, mean and scale in float,
+ * y = x * scale; then ggml_mul by the [n] weight when w is given. The reference
+ * test restates it at tests/attn_test.rs:278-283 (float sum, division by the
+ * root); ggml's own order is followed here. */
+void orc_rms_norm_mul_row(const float *x, const float *w, float eps, int64_t n, float *y) {
+    double sum = 0.0;
+    for (int64_t i = 0; i < n; ++i) sum += (double)(x[i] * x[i]);
+    const float mean = (float)(sum / (double)n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int64_t i = 0; i < n; ++i) {
+        y[i] = x[i] * scale;
+        if (w) y[i] = y[i] * w[i];
+    }
+}
+
+/* IMROPE cos/sin of the n_rot/2 rotation pairs of one token: ggml's
+ * mrope cache with the interleaved sector rule, restated at
+ * tests/attn_test.rs:153-193 (rope_ref). The four angles start at the token's
+ * positions and are multiplied by theta_scale = freq_base^(-2/n_rot) once per
+ * pair, in float, as ggml does; pair ic takes the angle of its sector:
+ * h when ic%S%3 == 1 and ic%S < 3*s1, w when 2 and < 3*s2, t when 0 and < 3*s0,
+ * else e (S = s0+s1+s2+s3). With ext_factor 0 (rope_yarn without ramp):
+ * cos = cosf(freq_scale*theta)*attn_factor, sin likewise. */
+void orc_imrope_cache(int32_t n_rot, const int32_t sections[4], float theta_scale, float freq_scale,
+                      float attn_factor, const int32_t p[4], float *cache) {
+    const int32_t sect = sections[0] + sections[1] + sections[2] + sections[3];
+    float th_t = (float)p[0], th_h = (float)p[1], th_w = (float)p[2], th_e = (float)p[3];
+    for (int32_t i0 = 0; i0 < n_rot; i0 += 2) {
+        const int32_t sector = (i0 / 2) % sect;
+        float theta;
+        if (sector % 3 == 1 && sector < 3 * sections[1]) theta = th_h;
+        else if (sector % 3 == 2 && sector < 3 * sections[2]) theta = th_w;
+        else if (sector % 3 == 0 && sector < 3 * sections[0]) theta = th_t;
+        else theta = th_e;
+        const float th = freq_scale * theta;
+        cache[i0] = cosf(th) * attn_factor;
+        cache[i0 + 1] = sinf(th) * attn_factor;
+        th_t *= theta_scale;
+        th_h *= theta_scale;
+        th_w *= theta_scale;
+        th_e *= theta_scale;
+    }
+}
+
+/* Rotation of one head row: pairs (ic, ic + n_rot/2) for ic < n_rot/2 (the
+ * NEOX-style pairing of mrope), dims >= n_rot copied (attn_test.rs:195-205). */
+void orc_rope_row(const float *x, int64_t n, int32_t n_rot, const float *cache, float *y) {
+    const int32_t half = n_rot / 2;
+    for (int64_t i = n_rot; i < n; ++i) y[i] = x[i];
+    for (int32_t ic = 0; ic < half; ++ic) {
+        const float ct = cache[2 * ic], st = cache[2 * ic + 1];
+        const float x0 = x[ic], x1 = x[ic + half];
+        y[ic] = x0 * ct - x1 * st;
+        y[ic + half] = x0 * st + x1 * ct;
+    }
+}
+
+static int producer_check(const sqa_tensor *src, const sqa_tensor *norm_w, const sqa_tensor *pos,
+                          const sqa_rope *rope) {
+    if (!src || !pos || !rope || src->type != SQA_TYPE_F32 || pos->type != SQA_TYPE_I32) return SQA_ERR_INVALID;
+    if (norm_w && (norm_w->type != SQA_TYPE_F32 || norm_w->ne[0] != src->ne[0])) return SQA_ERR_INVALID;
+    if (pos->ne[0] != 4 * src->ne[2] || rope->n_rot <= 0 || rope->n_rot % 2 || rope->n_rot > src->ne[0])
+        return SQA_ERR_INVALID;
+    if (rope->sections[0] + rope->sections[1] + rope->sections[2] + rope->sections[3] <= 0) return SQA_ERR_INVALID;
+    if (rope->ext_factor != 0.0f) return SQA_ERR_UNSUPPORTED;
+    return SQA_OK;
+}
+
+/* One token-head row through norm and rope into y (n floats). */
+static void producer_row(const sqa_tensor *src, const sqa_tensor *norm_w, float eps, const sqa_tensor *pos,
+                         const sqa_rope *rope, float theta_scale, int64_t t, int64_t h, float *y) {
+    const int64_t n = src->ne[0], n_tok = src->ne[2];
+    const float *x = (const float *)((const char *)src->data + h * src->nb[1] + t * src->nb[2]);
+    float *tmp = (float *)malloc((size_t)n * sizeof(float));
+    float *cache = (float *)malloc((size_t)rope->n_rot * sizeof(float));
+    if (norm_w) orc_rms_norm_mul_row(x, (const float *)norm_w->data, eps, n, tmp);
+    else memcpy(tmp, x, (size_t)n * sizeof(float));
+    const int32_t *pp = (const int32_t *)pos->data;
+    const int32_t p[4] = {pp[t], pp[t + n_tok], pp[t + 2 * n_tok], pp[t + 3 * n_tok]};
+    orc_imrope_cache(rope->n_rot, rope->sections, theta_scale, rope->freq_scale, rope->attn_factor, p, cache);
+    orc_rope_row(tmp, n, rope->n_rot, cache, y);
+    free(cache);
+    free(tmp);
+}
+
+float orc_rope_theta_scale(const sqa_rope *rope) { return powf(rope->freq_base, -2.0f / (float)rope->n_rot); }
+
+int orc_rope_norm_set_rows_q4_0(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w,
+                                float eps, const sqa_tensor *pos, const sqa_rope *rope, const sqa_tensor *idx) {
+    const int st = producer_check(src, norm_w, pos, rope);
+    if (st != SQA_OK) return st;
+    if (!dst || !idx || dst->type != SQA_TYPE_Q4_0 || idx->type != SQA_TYPE_I64) return SQA_ERR_INVALID;
+    const int64_t n = src->ne[0], n_head = src->ne[1], n_tok = src->ne[2];
+    if (n % SQA_QK4_0 || dst->ne[0] != n * n_head || idx->ne[0] != n_tok) return SQA_ERR_INVALID;
+    const float ts = orc_rope_theta_scale(rope);
+    float *y = (float *)malloc((size_t)n * sizeof(float));
+    for (int64_t t = 0; t < n_tok; ++t) {
+        const int64_t r = *(const int64_t *)((const char *)idx->data + t * idx->nb[0]);
+        if (r < 0 || r >= dst->ne[1]) continue;
+        for (int64_t h = 0; h < n_head; ++h) {
+            producer_row(src, norm_w, eps, pos, rope, ts, t, h, y);
+            orc_quantize_row_q4_0(y, (uint8_t *)dst->data + r * dst->nb[1] + h * (n / SQA_QK4_0) * SQA_Q4_0_BLOCK_BYTES,
+                                  n);
+        }
+    }
+    free(y);
+    return SQA_OK;
+}
+
+int orc_rope_norm_f32(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w, float eps,
+                      const sqa_tensor *pos, const sqa_rope *rope) {
+    const int st = producer_check(src, norm_w, pos, rope);
+    if (st != SQA_OK) return st;
+    if (!dst || dst->type != SQA_TYPE_F32) return SQA_ERR_INVALID;
+    const int64_t n = src->ne[0], n_head = src->ne[1], n_tok = src->ne[2];
+    const float ts = orc_rope_theta_scale(rope);
+    for (int64_t t = 0; t < n_tok; ++t)
+        for (int64_t h = 0; h < n_head; ++h)
+            producer_row(src, norm_w, eps, pos, rope, ts, t, h, (float *)dst->data + (t * n_head + h) * n);
+    return SQA_OK;
+}
+
 int orc_max_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

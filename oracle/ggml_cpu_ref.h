@@ -25,6 +25,14 @@
  *                                          src/model/graph.rs:486-576 and the gate of
  *                                          src/model/attn.rs:282-283
  *   orc_sigmoid_mul                      - ggml_sigmoid + ggml_mul (src/model/attn.rs:282-283)
+ *   orc_rms_norm_mul_row                 - ggml_rms_norm + ggml_mul of head_rms_norm
+ *                                          (src/model/attn.rs:68-84; test restatement
+ *                                          tests/attn_test.rs:278-283)
+ *   orc_imrope_cache / orc_rope_row      - ggml_rope_multi with GGML_ROPE_TYPE_IMROPE
+ *                                          (src/model/attn.rs:180-200; test restatement
+ *                                          rope_ref, tests/attn_test.rs:148-208)
+ *   orc_rope_norm_set_rows_q4_0          - norm -> rope -> set_rows for K, and
+ *   orc_rope_norm_f32                      norm -> rope for Q (src/model/attn.rs:166-200)
  */
 #ifndef GGML_CPU_REF_H
 #define GGML_CPU_REF_H
@@ -61,6 +69,15 @@ int orc_flash_attn_ext_causal(const sqa_tensor *q, const sqa_tensor *k, const sq
                               int64_t q_pos0, const sqa_tensor *gate, float scale,
                               const sqa_tensor *dst, int n_threads, int q8_variant);
 int orc_sigmoid_mul(const sqa_tensor *dst, const sqa_tensor *x, const sqa_tensor *gate);
+void orc_rms_norm_mul_row(const float *x, const float *w, float eps, int64_t n, float *y);
+void orc_imrope_cache(int32_t n_rot, const int32_t sections[4], float theta_scale, float freq_scale,
+                      float attn_factor, const int32_t p[4], float *cache);
+void orc_rope_row(const float *x, int64_t n, int32_t n_rot, const float *cache, float *y);
+float orc_rope_theta_scale(const sqa_rope *rope);
+int orc_rope_norm_set_rows_q4_0(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w,
+                                float eps, const sqa_tensor *pos, const sqa_rope *rope, const sqa_tensor *idx);
+int orc_rope_norm_f32(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w, float eps,
+                      const sqa_tensor *pos, const sqa_rope *rope);
 
 int orc_max_threads(void);
 

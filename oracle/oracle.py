@@ -20,7 +20,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_I64 = 0, 1, 2, 27
+TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_I32, TYPE_I64 = 0, 1, 2, 26, 27
 Q8_X86, Q8_SCALAR = 0, 1
 QK = 32
 Q4_BLOCK = 18
@@ -37,6 +37,28 @@ class Tensor(ctypes.Structure):
         ("nb", ctypes.c_uint64 * 4),
         ("data", ctypes.c_void_p),
     ]
+
+
+class Rope(ctypes.Structure):
+    """Same layout as sqa_rope in include/sqattn.h."""
+
+    _fields_ = [
+        ("n_rot", ctypes.c_int32),
+        ("sections", ctypes.c_int32 * 4),
+        ("freq_base", ctypes.c_float),
+        ("freq_scale", ctypes.c_float),
+        ("ext_factor", ctypes.c_float),
+        ("attn_factor", ctypes.c_float),
+    ]
+
+
+def rope_params(n_rot, sections, freq_base, freq_scale=1.0, ext_factor=0.0, attn_factor=1.0):
+    r = Rope()
+    r.n_rot = n_rot
+    for i in range(4):
+        r.sections[i] = sections[i]
+    r.freq_base, r.freq_scale, r.ext_factor, r.attn_factor = freq_base, freq_scale, ext_factor, attn_factor
+    return r
 
 
 def build(force=False):
@@ -70,6 +92,17 @@ def lib():
         L.orc_flash_attn_ext_causal.argtypes = [P, P, P, ctypes.c_int64, P, ctypes.c_float, P,
                                                 ctypes.c_int, ctypes.c_int]
         L.orc_sigmoid_mul.argtypes = [P, P, P]
+        R = ctypes.POINTER(Rope)
+        L.orc_rms_norm_mul_row.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_int64,
+                                           ctypes.c_void_p]
+        L.orc_imrope_cache.argtypes = [ctypes.c_int32, ctypes.c_void_p, ctypes.c_float, ctypes.c_float,
+                                       ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p]
+        L.orc_rope_row.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p,
+                                   ctypes.c_void_p]
+        L.orc_rope_theta_scale.restype = ctypes.c_float
+        L.orc_rope_theta_scale.argtypes = [R]
+        L.orc_rope_norm_set_rows_q4_0.argtypes = [P, P, P, ctypes.c_float, P, R, P]
+        L.orc_rope_norm_f32.argtypes = [P, P, P, ctypes.c_float, P, R]
         L.orc_max_threads.restype = ctypes.c_int
         _lib = L
     return _lib
@@ -223,3 +256,72 @@ def causal_mask(n_q, n_kv, step_start):
     for t in range(n_q):
         m[t, : min(step_start + t + 1, n_kv)] = 0
     return m
+
+
+# ----------------------------------------------------- K/Q producer (norm+rope) --
+
+def rms_norm_mul_row(x, w, eps):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.zeros_like(x)
+    wa = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
+    lib().orc_rms_norm_mul_row(_ptr(x), None if wa is None else _ptr(wa), eps, x.size, _ptr(y))
+    return y
+
+
+def imrope_cache(rope, p4):
+    """cos/sin pairs (n_rot,) of one token with positions p4 = (t, h, w, e)."""
+    sec = np.array(list(rope.sections), dtype=np.int32)
+    p = np.array(p4, dtype=np.int32)
+    cache = np.zeros(rope.n_rot, dtype=np.float32)
+    ts = lib().orc_rope_theta_scale(ctypes.byref(rope))
+    lib().orc_imrope_cache(rope.n_rot, _ptr(sec), ts, rope.freq_scale, rope.attn_factor, _ptr(p), _ptr(cache))
+    return cache
+
+
+def rope_row(x, rope, cache):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.zeros_like(x)
+    lib().orc_rope_row(_ptr(x), x.size, rope.n_rot, _ptr(cache), _ptr(y))
+    return y
+
+
+def _producer_tensors(src, norm_w, pos):
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    n_tok, n_head, D = src.shape
+    ts = tensor(TYPE_F32, [D, n_head, n_tok], [4, D * 4, n_head * D * 4], src)
+    tw = None
+    if norm_w is not None:
+        norm_w = np.ascontiguousarray(norm_w, dtype=np.float32)
+        tw = tensor(TYPE_F32, [D], [4], norm_w)
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    assert pos.shape == (4 * n_tok,)
+    tp = tensor(TYPE_I32, [4 * n_tok], [4], pos)
+    return (src, norm_w, pos), ts, tw, tp
+
+
+def rope_norm_set_rows_q4_0(cache, src, norm_w, eps, pos, rope, idx):
+    """cache uint8 (rows, n_head*D//32*18) updated in place; src f32 (n_tok, n_head, D);
+    pos int32 (4*n_tok,) t/h/w/e positions; idx int64 (n_tok,)."""
+    keep, ts, tw, tp = _producer_tensors(src, norm_w, pos)
+    n_tok, n_head, D = keep[0].shape
+    idx = np.ascontiguousarray(idx, dtype=np.int64)
+    rb = n_head * D // QK * Q4_BLOCK
+    assert cache.flags.c_contiguous and cache.dtype == np.uint8 and cache.shape[1] == rb
+    td = tensor(TYPE_Q4_0, [n_head * D, cache.shape[0]], [Q4_BLOCK, rb], cache)
+    ti = tensor(TYPE_I64, [n_tok], [8], idx)
+    rc = lib().orc_rope_norm_set_rows_q4_0(ctypes.byref(td), ctypes.byref(ts),
+                                           ctypes.byref(tw) if tw is not None else None, eps,
+                                           ctypes.byref(tp), ctypes.byref(rope), ctypes.byref(ti))
+    assert rc == 0, rc
+    return cache
+
+
+def rope_norm_f32(src, norm_w, eps, pos, rope):
+    keep, ts, tw, tp = _producer_tensors(src, norm_w, pos)
+    out = np.zeros_like(keep[0])
+    n_tok, n_head, D = out.shape
+    to = tensor(TYPE_F32, [D, n_head, n_tok], [4, D * 4, n_head * D * 4], out)
+    rc = lib().orc_rope_norm_f32(ctypes.byref(to), ctypes.byref(ts), ctypes.byref(tw) if tw is not None else None,
+                                 eps, ctypes.byref(tp), ctypes.byref(rope))
+    assert rc == 0, rc
+    return out

@@ -21,13 +21,13 @@ __all__ = [
     "Tensor", "lib", "last_error", "SqaError", "set_rows_q4_0", "flash_attn_ext",
     "flash_attn_ext_causal", "sigmoid_mul", "fill_causal_mask", "supports_flash_attn_ext",
     "flash_attn_workspace_size", "KvCache", "cache_view", "row_bytes", "profile_begin", "profile_end",
-    "profile_get",
+    "profile_get", "Rope", "rope_params", "rope_norm_set_rows_q4_0", "rope_norm_f32",
 ]
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libsqattn.so")
 
-TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_I64 = 0, 1, 2, 27
+TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_I32, TYPE_I64 = 0, 1, 2, 26, 27
 QK4_0 = 32
 Q4_0_BLOCK = 18
 KV_PAD = 256
@@ -67,6 +67,29 @@ class Tensor(ctypes.Structure):
         return t
 
 
+class Rope(ctypes.Structure):
+    """sqa_rope: the ggml_rope_multi parameters of RopeParams (reference attn.rs:30-65)."""
+
+    _fields_ = [
+        ("n_rot", ctypes.c_int32),
+        ("sections", ctypes.c_int32 * 4),
+        ("freq_base", ctypes.c_float),
+        ("freq_scale", ctypes.c_float),
+        ("ext_factor", ctypes.c_float),
+        ("attn_factor", ctypes.c_float),
+    ]
+
+
+def rope_params(n_rot, sections, freq_base, freq_scale=1.0, ext_factor=0.0, attn_factor=1.0):
+    """RopeParams::text (reference attn.rs:46-64): no YaRN ramp, attn_factor 1."""
+    r = Rope()
+    r.n_rot = int(n_rot)
+    for i in range(4):
+        r.sections[i] = int(sections[i])
+    r.freq_base, r.freq_scale, r.ext_factor, r.attn_factor = freq_base, freq_scale, ext_factor, attn_factor
+    return r
+
+
 _lib = None
 
 
@@ -85,6 +108,8 @@ def lib():
             "sqa_status_string": (ctypes.c_char_p, [ctypes.c_int]),
             "sqa_set_rows_q4_0": (ctypes.c_int, [P, P, P, vp]),
             "sqa_supports_set_rows": (ctypes.c_int, [P, P, P]),
+            "sqa_rope_norm_set_rows_q4_0": (ctypes.c_int, [P, P, P, f32, P, ctypes.POINTER(Rope), P, vp]),
+            "sqa_rope_norm_f32": (ctypes.c_int, [P, P, P, f32, P, ctypes.POINTER(Rope), vp]),
             "sqa_flash_attn_ext": (ctypes.c_int, [P, P, P, P, f32, f32, f32, P, vp, sz, vp]),
             "sqa_flash_attn_ext_workspace_size": (sz, [P, P, P, P]),
             "sqa_supports_flash_attn_ext": (ctypes.c_int, [P, P, P, P, f32, f32, f32, P]),
@@ -186,6 +211,43 @@ def set_rows_q4_0(cache, src, idx, stream=None):
     ti = Tensor.make(TYPE_I64, [idx.shape[0]], [idx.stride(0) * 8], idx.data_ptr())
     _check(lib().sqa_set_rows_q4_0(ctypes.byref(td), ctypes.byref(ts), ctypes.byref(ti), _stream(stream)))
     return cache
+
+
+def _producer_descs(src, norm_w, pos):
+    n_tok, n_head, D = src.shape
+    ts = Tensor.make(TYPE_F32, [D, n_head, n_tok], [4, src.stride(1) * 4, src.stride(0) * 4], src.data_ptr())
+    tw = None if norm_w is None else Tensor.make(TYPE_F32, [D], [4], norm_w.data_ptr())
+    tp = Tensor.make(TYPE_I32, [pos.shape[0]], [4], pos.data_ptr())
+    return ts, tw, tp
+
+
+def rope_norm_set_rows_q4_0(cache, src, norm_w, eps, pos, rope, idx, stream=None):
+    """K producer (reference attn.rs:166-200 + kv.rs:313-399): per-head RMSNorm times
+    norm_w, IMROPE with positions pos, q4_0 quantize-on-write into cache rows idx.
+
+    cache: uint8 (rows, ..., n_head*D//32*18) contiguous; src: float32 (n_tok, n_head, D)
+    with contiguous rows; norm_w: float32 (D,) or None; pos: int32 (4*n_tok,);
+    idx: int64 (n_tok,)."""
+    n_tok, n_head, D = src.shape
+    rows = cache.shape[0]
+    rb = cache[0].numel()
+    assert rb == n_head * D // QK4_0 * Q4_0_BLOCK, "row length mismatch"
+    ts, tw, tp = _producer_descs(src, norm_w, pos)
+    td = Tensor.make(TYPE_Q4_0, [n_head * D, rows], [Q4_0_BLOCK, rb], cache.data_ptr())
+    ti = Tensor.make(TYPE_I64, [idx.shape[0]], [idx.stride(0) * 8], idx.data_ptr())
+    _check(lib().sqa_rope_norm_set_rows_q4_0(ctypes.byref(td), ctypes.byref(ts), _ref(tw), eps, ctypes.byref(tp),
+                                             ctypes.byref(rope), ctypes.byref(ti), _stream(stream)))
+    return cache
+
+
+def rope_norm_f32(out, src, norm_w, eps, pos, rope, stream=None):
+    """Q producer (reference attn.rs:166-199): out float32 (n_tok, n_head, D) contiguous."""
+    n_tok, n_head, D = src.shape
+    ts, tw, tp = _producer_descs(src, norm_w, pos)
+    to = Tensor.make(TYPE_F32, [D, n_head, n_tok], [4, D * 4, n_head * D * 4], out.data_ptr())
+    _check(lib().sqa_rope_norm_f32(ctypes.byref(to), ctypes.byref(ts), _ref(tw), eps, ctypes.byref(tp),
+                                   ctypes.byref(rope), _stream(stream)))
+    return out
 
 
 def flash_attn_workspace_size(q, k_cache, n_kv):

@@ -179,6 +179,74 @@ int sqa_set_rows_q4_0(const sqa_tensor *dst, const sqa_tensor *src, const sqa_te
     return launch_set_rows_q4_0(*dst, *src, *idx, (hipStream_t)stream);
 }
 
+// ---- K/Q producer: norm + IMROPE (+ q4_0 set_rows) ----------------------------
+
+static int check_producer(const sqa_tensor *src, const sqa_tensor *norm_w, const sqa_tensor *pos,
+                          const sqa_rope *rope, const char *what) {
+    if (!src || !pos || !rope) return set_error(SQA_ERR_INVALID, "%s: null argument", what);
+    if (src->type != SQA_TYPE_F32 || pos->type != SQA_TYPE_I32)
+        return set_error(SQA_ERR_INVALID, "%s: src must be F32 and pos I32", what);
+    const int64_t D = src->ne[0], n_tok = src->ne[2];
+    if (src->ne[3] != 1 || pos->ne[0] != 4 * n_tok || pos->nb[0] != 4)
+        return set_error(SQA_ERR_INVALID, "%s: pos must be I32 [4 * n_tok] contiguous", what);
+    if (n_tok > 0 && (!src->data || !pos->data)) return set_error(SQA_ERR_INVALID, "%s: null data pointer", what);
+    if (D != 64 && D != 128 && D != 256)
+        return set_error(SQA_ERR_UNSUPPORTED, "%s: head dim %lld not in {64, 128, 256}", what, (long long)D);
+    if (src->nb[0] != 4 || src->nb[1] % 4 || src->nb[2] % 4 || (uintptr_t)src->data % 4)
+        return set_error(SQA_ERR_UNSUPPORTED, "%s: src elements must be contiguous F32", what);
+    if (norm_w && (norm_w->type != SQA_TYPE_F32 || norm_w->ne[0] != D || norm_w->nb[0] != 4 ||
+                   (uintptr_t)norm_w->data % 16))
+        return set_error(SQA_ERR_INVALID, "%s: norm weight must be F32 [D], contiguous, 16-byte aligned", what);
+    if (rope->n_rot <= 0 || rope->n_rot % 8 || rope->n_rot > D)
+        return set_error(SQA_ERR_UNSUPPORTED, "%s: n_rot %d must be a positive multiple of 8 <= D", what,
+                         rope->n_rot);
+    int sect = 0;
+    for (int k = 0; k < 4; ++k) {
+        if (rope->sections[k] < 0) return set_error(SQA_ERR_INVALID, "%s: negative rope section", what);
+        sect += rope->sections[k];
+    }
+    if (sect <= 0) return set_error(SQA_ERR_INVALID, "%s: rope sections sum to zero", what);
+    if (rope->ext_factor != 0.0f)
+        return set_error(SQA_ERR_UNSUPPORTED, "%s: ext_factor != 0 (YaRN ramp) is not supported", what);
+    if (!std::isfinite(rope->freq_base) || rope->freq_base <= 0.0f)
+        return set_error(SQA_ERR_INVALID, "%s: freq_base must be positive", what);
+    return SQA_OK;
+}
+
+int sqa_rope_norm_set_rows_q4_0(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w,
+                                float eps, const sqa_tensor *pos, const sqa_rope *rope,
+                                const sqa_tensor *idx, void *stream) {
+    const char *what = "rope_norm_set_rows_q4_0";
+    int st = check_producer(src, norm_w, pos, rope, what);
+    if (st != SQA_OK) return st;
+    if (!dst || !idx) return set_error(SQA_ERR_INVALID, "%s: null dst or idx", what);
+    if (dst->type != SQA_TYPE_Q4_0 || idx->type != SQA_TYPE_I64)
+        return set_error(SQA_ERR_INVALID, "%s: dst must be Q4_0 and idx I64", what);
+    const int64_t D = src->ne[0], n_head = src->ne[1], n_tok = src->ne[2];
+    if (dst->ne[0] != D * n_head || idx->ne[0] != n_tok)
+        return set_error(SQA_ERR_INVALID, "%s: dst row must hold n_head * D values, idx n_tok entries", what);
+    if (dst->nb[0] != SQA_Q4_0_BLOCK_BYTES || dst->nb[1] % 2 || (uintptr_t)dst->data % 2 || idx->nb[0] % 8)
+        return set_error(SQA_ERR_UNSUPPORTED, "%s: dst/idx strides not supported", what);
+    if (n_tok > 0 && (!dst->data || !idx->data)) return set_error(SQA_ERR_INVALID, "%s: null data pointer", what);
+    const float ts = powf(rope->freq_base, -2.0f / (float)rope->n_rot);
+    return launch_rope_norm(dst, *src, norm_w, eps, *pos, *rope, ts, idx, (hipStream_t)stream);
+}
+
+int sqa_rope_norm_f32(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w, float eps,
+                      const sqa_tensor *pos, const sqa_rope *rope, void *stream) {
+    const char *what = "rope_norm_f32";
+    int st = check_producer(src, norm_w, pos, rope, what);
+    if (st != SQA_OK) return st;
+    if (!dst || dst->type != SQA_TYPE_F32) return set_error(SQA_ERR_INVALID, "%s: dst must be F32", what);
+    const int64_t D = src->ne[0], n_head = src->ne[1], n_tok = src->ne[2];
+    if (dst->ne[0] != D || dst->ne[1] != n_head || dst->ne[2] != n_tok || dst->nb[0] != 4 ||
+        dst->nb[1] != (uint64_t)(4 * D) || dst->nb[2] != (uint64_t)(4 * D * n_head) || (uintptr_t)dst->data % 16)
+        return set_error(SQA_ERR_INVALID, "%s: dst must be F32 [D, n_head, n_tok] contiguous, 16-byte aligned",
+                         what);
+    const float ts = powf(rope->freq_base, -2.0f / (float)rope->n_rot);
+    return launch_rope_norm(dst, *src, norm_w, eps, *pos, *rope, ts, nullptr, (hipStream_t)stream);
+}
+
 size_t sqa_flash_attn_ext_workspace_size(const sqa_tensor *q, const sqa_tensor *k,
                                          const sqa_tensor *v, const sqa_tensor *dst) {
     bool decode = false;

@@ -30,6 +30,11 @@ void profile_stop(int slot, hipStream_t s);
 // Kernel launchers (defined next to their kernels).
 int launch_set_rows_q4_0(const sqa_tensor &dst, const sqa_tensor &src, const sqa_tensor &idx,
                          hipStream_t s);
+// Norm + IMROPE producer; idx != null: q4_0 quantize-on-write into dst rows,
+// else F32 output (rope_norm_q4_0.hip). theta_scale = powf(freq_base, -2/n_rot).
+int launch_rope_norm(const sqa_tensor *dst, const sqa_tensor &src, const sqa_tensor *norm_w, float eps,
+                     const sqa_tensor &pos, const sqa_rope &rope, float theta_scale, const sqa_tensor *idx,
+                     hipStream_t s);
 int launch_sigmoid_mul(const sqa_tensor &dst, const sqa_tensor &x, const sqa_tensor &gate,
                        hipStream_t s);
 int launch_fill_causal_mask(const sqa_tensor &mask, int64_t step_start, hipStream_t s);

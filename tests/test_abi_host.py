@@ -138,3 +138,35 @@ def test_kv_cache_create_rejects_bad_geometry(sqa):
     assert "multiple of 32" in sqa.last_error()
     nul = (ctypes.c_void_p * 1)(None)
     assert not L.sqa_kv_cache_create(1, 256, 2, 256, bufs, nul)
+
+
+def test_producer_argument_checks_before_any_launch(sqa):
+    """rope_norm entry points reject what they do not run (YaRN ramp, odd n_rot,
+    head dims outside {64, 128, 256}, short pos, mismatched dst) with a status
+    and a message, without touching the device (fake non-null pointers)."""
+    L = sqa.lib()
+    T = sqa.Tensor.make
+    D, n_head, n_tok = 256, 2, 8
+    src = T(0, [D, n_head, n_tok], [4, D * 4, n_head * D * 4], 4096)
+    w = T(0, [D], [4], 8192)
+    pos = T(26, [4 * n_tok], [4], 12288)
+    idx = T(27, [n_tok], [8], 16384)
+    dst = T(2, [n_head * D, 64], [18, n_head * D // 32 * 18], 32768)
+    by = ctypes.byref
+
+    def call(rope, s=src, p=pos, d=dst, i=idx, ww=w):
+        return L.sqa_rope_norm_set_rows_q4_0(by(d), by(s), by(ww) if ww else None, 1e-6, by(p), by(rope),
+                                             by(i), None)
+
+    good = sqa.rope_params(64, (11, 11, 10, 0), 1e7)
+    yarn = sqa.rope_params(64, (11, 11, 10, 0), 1e7, ext_factor=1.0)
+    assert call(yarn) == 2 and b"ext_factor" in L.sqa_last_error()
+    assert call(sqa.rope_params(12, (3, 3, 0, 0), 1e7)) == 2           # n_rot % 8
+    assert call(sqa.rope_params(64, (0, 0, 0, 0), 1e7)) == 1            # empty sections
+    assert call(good, p=T(26, [4 * n_tok - 1], [4], 12288)) == 1        # short pos
+    assert call(good, d=T(2, [D, 64], [18, 144], 32768)) == 1           # dst row of one head
+    assert call(good, s=T(0, [96, n_head, n_tok], [4, 384, 768], 4096),
+                d=T(2, [96 * n_head, 64], [18, 108], 32768)) == 2        # head dim 96
+    assert call(good, ww=T(0, [D], [4], 8196)) == 1                     # unaligned weight
+    out = T(0, [D, n_head, n_tok], [4, D * 4, n_head * D * 4], 65536)
+    assert L.sqa_rope_norm_f32(by(out), by(src), by(w), 1e-6, by(pos), by(yarn), None) == 2
