@@ -197,6 +197,52 @@ def stack_leg(sqa, torch, dev, steps, warmup):
     return res
 
 
+def producer_leg(sqa, torch, dev, steps, warmup):
+    """K/Q producer per layer: RMSNorm + IMROPE + q4_0 quantize-on-write of the new
+    K rows (2 KV heads), and RMSNorm + IMROPE of Q (16 heads, F32 out), for a
+    512-token and a 2048-token ubatch. n_rot 64, sections (11, 11, 10, 0),
+    freq_base 1e7 (plausible model values; the kernel takes them as parameters)."""
+    rope = sqa.rope_params(64, (11, 11, 10, 0), 1e7)
+    out = {}
+    for n_tok, start in ((PP_N_Q, PP_START), (2048, 131072)):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(n_tok)
+        k_src = torch.randn((n_tok, HKV, D), generator=gen, device=dev)
+        q_src = torch.randn((n_tok, H, D), generator=gen, device=dev)
+        kw = torch.randn((D,), generator=gen, device=dev)
+        qw = torch.randn((D,), generator=gen, device=dev)
+        t = torch.arange(start, start + n_tok, device=dev, dtype=torch.int32)
+        pos = t.repeat(4)
+        idx = t.to(torch.int64)
+        cache = torch.zeros((start + n_tok, HKV, D // 32 * 18), dtype=torch.uint8, device=dev)
+        q_out = torch.empty_like(q_src)
+
+        def step():
+            for _ in range(N_LAYERS):
+                sqa.rope_norm_set_rows_q4_0(cache, k_src, kw, 1e-6, pos, rope, idx)
+                sqa.rope_norm_f32(q_out, q_src, qw, 1e-6, pos, rope)
+
+        for _ in range(warmup):
+            step()
+        ms = time_steps(torch, step, steps) / steps
+        sqa.profile_begin(steps * N_LAYERS * 2 + 8)
+        time_steps(torch, step, steps)
+        sqa.profile_end()
+        kern = {}
+        for name in ("rope_norm_set_rows_q4_0", "rope_norm_f32"):
+            tt, c = sqa.profile_get(name)
+            kern[name] = round(tt / c * 1e3, 2)
+        k_bytes = n_tok * HKV * (D * 4 + 288 // HKV) + n_tok * (16 + 8)
+        q_bytes = n_tok * H * D * 8 + n_tok * 16
+        out[f"ubatch{n_tok}"] = {
+            "per_layer_us": round(ms * 1e3 / N_LAYERS, 2), "kernels_us": kern,
+            "k_GB/s": round(k_bytes / (kern["rope_norm_set_rows_q4_0"] * 1e-6) / 1e9, 1),
+            "q_GB/s": round(q_bytes / (kern["rope_norm_f32"] * 1e-6) / 1e9, 1),
+            "bytes": {"k": k_bytes, "q": q_bytes}}
+        del k_src, q_src, cache, q_out
+    return out
+
+
 def cpu_baseline(orc, kq, vq, q, mask, budget_s=8.0):
     """The oracle (C restatement of ggml's CPU flash_attn_ext) on this host."""
     threads = min(os.cpu_count() or 1, 16, q.shape[0] * q.shape[1])
@@ -223,6 +269,7 @@ def main():
     ap.add_argument("--no-verify", action="store_true", help="skip the n_q=2 verify leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the pp512 prefill leg")
     ap.add_argument("--no-stack", action="store_true", help="skip the 10-layer ubatch-2048 stack leg")
+    ap.add_argument("--no-producer", action="store_true", help="skip the K/Q producer (norm + rope) leg")
     ap.add_argument("--copy-ref", action="store_true",
                     help="run a plain 256 MiB device copy at the end (counter calibration)")
     args = ap.parse_args()
@@ -318,6 +365,9 @@ def main():
         torch.cuda.empty_cache()
     if not args.no_stack:
         result["stack_ub2048_131k"] = stack_leg(sqa, torch, dev, 2, 1)
+        torch.cuda.empty_cache()
+    if not args.no_producer:
+        result["producer_rope_norm"] = producer_leg(sqa, torch, dev, max(2, args.steps // 2), 2)
         torch.cuda.empty_cache()
 
     if not args.no_cpu:

@@ -18,10 +18,11 @@
 //         (x0*c - x1*s, x0*s + x1*c); dims >= n_rot pass through;
 //   q4_0: ggml's quantize_row_q4_0_ref (q4_0_block.hpp).
 //
-// Layout: D/4 lanes per head row, 4 consecutive dims each, so the 8 lanes of a
-// 32-value block hold it as the quantizer wants; a 256-thread workgroup takes
-// 256/(D/4) rows (token, head). The rotation partner of dim d sits in the same
-// register of the lane n_rot/8 away (n_rot % 8 == 0).
+// Layout: one workgroup per token. Its first n_rot/2 threads form the token's
+// cos/sin table in LDS (as ggml forms one cache per token), then the heads stream
+// through D/4 lanes per head row, 4 consecutive dims each, so the 8 lanes of a
+// 32-value block hold it as the quantizer wants. The rotation partner of dim d
+// sits in the same register of the lane n_rot/8 away (n_rot % 8 == 0).
 #include "q4_0_block.hpp"
 
 namespace sqa {
@@ -52,90 +53,94 @@ struct ProducerParams {
 
 template <int D, bool kQ4, bool kVec>
 __global__ __launch_bounds__(kThreads) void rope_norm_kernel(ProducerParams p) {
-    constexpr int kLanes = D / 4;  // lanes per head row
+    constexpr int kLanes = D / 4;                  // lanes per head row
+    constexpr int kRowsPerPass = kThreads / kLanes;  // head rows in flight
+    __shared__ float2 cs[D / 2];                   // (cos, sin) of rotation pair ic
     const int tid = threadIdx.x;
-    const int l = tid % kLanes;
-    const int64_t row = (int64_t)blockIdx.x * (kThreads / kLanes) + tid / kLanes;
-    if (row >= p.n_tok * p.n_head) return;  // whole row groups exit together
-    const int64_t t = row / p.n_head;
-    const int h = (int)(row - t * p.n_head);
-    int64_t r = 0;
-    if constexpr (kQ4) {
-        r = *reinterpret_cast<const int64_t *>(p.idx + t * p.idx_nb0);
-        if (r < 0 || r >= p.dst_rows) return;  // same row for the whole group
-    }
-
-    const float *x = reinterpret_cast<const float *>(p.src + h * p.src_nb1 + t * p.src_nb2) + 4 * l;
-    float v[4];
-    if constexpr (kVec) {
-        const float4 f = *reinterpret_cast<const float4 *>(x);
-        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-    } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = x[j];
-    }
-
-    if (p.norm_w) {
-        double s = 0.0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) s += (double)__fmul_rn(v[j], v[j]);
-#pragma unroll
-        for (int off = kLanes / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, kLanes);
-        const float mean = (float)(s / (double)D);
-        const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, p.eps)));
-        const float4 w = *reinterpret_cast<const float4 *>(p.norm_w + 4 * l);
-        const float wv[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = __fmul_rn(__fmul_rn(v[j], scale), wv[j]);
-    }
-
-    // rotation: pair ic = (d, d + half) for d < half
+    const int64_t t = blockIdx.x;
     const int half = p.n_rot >> 1;
-    const int sh = half >> 2;  // lanes between the two dims of a pair
-    const int lp = 4 * l < half ? l + sh : (4 * l < p.n_rot ? l - sh : l);
-    float pos4[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) pos4[k] = (float)p.pos[t + k * p.n_tok];
-    float out[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float pv = __shfl(v[j], lp, kLanes);  // every lane takes part
-        const int d = 4 * l + j;
-        if (d >= p.n_rot) {
-            out[j] = v[j];
-            continue;
-        }
-        const bool first = d < half;
-        const int ic = first ? d : d - half;
+
+    // ---- the token's rotation table: pair ic, angle pos[sector] * theta_scale^ic
+    if (tid < half) {
+        const int ic = tid;
         const int sector = ic % p.sect;
         int c;  // position component: 0 t, 1 h, 2 w, 3 e
         if (sector % 3 == 1 && sector < 3 * p.sections[1]) c = 1;
         else if (sector % 3 == 2 && sector < 3 * p.sections[2]) c = 2;
         else if (sector % 3 == 0 && sector < 3 * p.sections[0]) c = 0;
         else c = 3;
-        float th = pos4[c];
+        float th = (float)p.pos[t + c * p.n_tok];
         for (int k = 0; k < ic; ++k) th = __fmul_rn(th, p.theta_scale);
         const float ang = __fmul_rn(p.freq_scale, th);
-        const float ct = __fmul_rn(cosf(ang), p.attn_factor);
-        const float st = __fmul_rn(sinf(ang), p.attn_factor);
-        out[j] = first ? __fsub_rn(__fmul_rn(v[j], ct), __fmul_rn(pv, st))   // x0*c - x1*s
-                       : __fadd_rn(__fmul_rn(pv, st), __fmul_rn(v[j], ct));  // x0*s + x1*c
+        float sn, cn;
+        sincosf(ang, &sn, &cn);  // one argument reduction for both
+        cs[ic] = make_float2(__fmul_rn(cn, p.attn_factor), __fmul_rn(sn, p.attn_factor));
     }
+    __syncthreads();
 
+    int64_t r = 0;
     if constexpr (kQ4) {
-        const int b = l >> 3;  // block of this lane's dims within the head row
-        quantize_q4_0_block8(out, l & 7,
-                             p.dst + r * p.dst_nb1 + (int64_t)(h * (D / SQA_QK4_0) + b) * SQA_Q4_0_BLOCK_BYTES);
-    } else {
-        *reinterpret_cast<float4 *>(p.dst_f32 + (t * p.n_head + h) * D + 4 * l) =
-            make_float4(out[0], out[1], out[2], out[3]);
+        r = *reinterpret_cast<const int64_t *>(p.idx + t * p.idx_nb0);
+        if (r < 0 || r >= p.dst_rows) return;  // whole workgroup, past its only barrier
+    }
+    const int l = tid % kLanes;
+    const int sh = half >> 2;  // lanes between the two dims of a pair
+    const int lp = 4 * l < half ? l + sh : (4 * l < p.n_rot ? l - sh : l);
+    for (int h = tid / kLanes; h < p.n_head; h += kRowsPerPass) {  // uniform per row group
+        const float *x = reinterpret_cast<const float *>(p.src + h * p.src_nb1 + t * p.src_nb2) + 4 * l;
+        float v[4];
+        if constexpr (kVec) {
+            const float4 f = *reinterpret_cast<const float4 *>(x);
+            v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = x[j];
+        }
+
+        if (p.norm_w) {
+            double s = 0.0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s += (double)__fmul_rn(v[j], v[j]);
+#pragma unroll
+            for (int off = kLanes / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, kLanes);
+            const float mean = (float)(s / (double)D);
+            const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, p.eps)));
+            const float4 w = *reinterpret_cast<const float4 *>(p.norm_w + 4 * l);
+            const float wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = __fmul_rn(__fmul_rn(v[j], scale), wv[j]);
+        }
+
+        float out[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float pv = __shfl(v[j], lp, kLanes);  // every lane takes part
+            const int d = 4 * l + j;
+            if (d >= p.n_rot) {
+                out[j] = v[j];
+            } else if (d < half) {
+                const float2 c = cs[d];  // x0 = v, x1 = partner: x0*c - x1*s
+                out[j] = __fsub_rn(__fmul_rn(v[j], c.x), __fmul_rn(pv, c.y));
+            } else {
+                const float2 c = cs[d - half];  // x0 = partner, x1 = v: x0*s + x1*c
+                out[j] = __fadd_rn(__fmul_rn(pv, c.y), __fmul_rn(v[j], c.x));
+            }
+        }
+
+        if constexpr (kQ4) {
+            const int b = l >> 3;  // block of this lane's dims within the head row
+            quantize_q4_0_block8(out, l & 7,
+                                 p.dst + r * p.dst_nb1 + (int64_t)(h * (D / SQA_QK4_0) + b) * SQA_Q4_0_BLOCK_BYTES);
+        } else {
+            *reinterpret_cast<float4 *>(p.dst_f32 + (t * p.n_head + h) * D + 4 * l) =
+                make_float4(out[0], out[1], out[2], out[3]);
+        }
     }
 }
 
 template <int D, bool kQ4>
 void launch_d(const ProducerParams &p, bool vec, hipStream_t s) {
-    const int64_t rows = p.n_tok * p.n_head;
-    const int64_t grid = (rows + kThreads / (D / 4) - 1) / (kThreads / (D / 4));
+    const int64_t grid = p.n_tok;  // one workgroup per token
     if (vec)
         rope_norm_kernel<D, kQ4, true><<<dim3((unsigned)grid), dim3(kThreads), 0, s>>>(p);
     else
