@@ -341,6 +341,23 @@ def main():
                      "bytes_per_launch": layer_bytes(N_KV, 1)},
     }
 
+    # The same 10-layer step captured once in a HIP graph and replayed: the
+    # reference keeps the step's pointers fixed so that ggml-cuda replays its
+    # graph. Reported beside the eager figure; `value` stays the eager one.
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    for _ in range(3):
+        graph.replay()
+    ms_g = time_steps(torch, graph.replay, args.steps) / args.steps
+    result["decode_graph_replay"] = {"per_layer_us": round(ms_g * 1e3 / N_LAYERS, 2),
+                                     "GB/s": round(bytes_step / (ms_g * 1e-3) / 1e9, 1)}
+    del graph
+
     if not args.no_verify:
         # MTP verify: n_q = 2 with the causal mask across the two rows.
         q2 = torch.randn((2, H, D), device=dev, dtype=torch.float32)
