@@ -270,6 +270,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the pp512 prefill leg")
     ap.add_argument("--no-stack", action="store_true", help="skip the 10-layer ubatch-2048 stack leg")
     ap.add_argument("--no-producer", action="store_true", help="skip the K/Q producer (norm + rope) leg")
+    ap.add_argument("--no-graph", action="store_true", help="skip the graph-replay decode timing")
     ap.add_argument("--copy-ref", action="store_true",
                     help="run a plain 256 MiB device copy at the end (counter calibration)")
     args = ap.parse_args()
@@ -344,19 +345,20 @@ def main():
     # The same 10-layer step captured once in a HIP graph and replayed: the
     # reference keeps the step's pointers fixed so that ggml-cuda replays its
     # graph. Reported beside the eager figure; `value` stays the eager one.
-    graph = torch.cuda.CUDAGraph()
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        with torch.cuda.graph(graph, stream=side):
-            step()
-    torch.cuda.current_stream().wait_stream(side)
-    for _ in range(3):
-        graph.replay()
-    ms_g = time_steps(torch, graph.replay, args.steps) / args.steps
-    result["decode_graph_replay"] = {"per_layer_us": round(ms_g * 1e3 / N_LAYERS, 2),
-                                     "GB/s": round(bytes_step / (ms_g * 1e-3) / 1e9, 1)}
-    del graph
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        for _ in range(3):
+            graph.replay()
+        ms_g = time_steps(torch, graph.replay, args.steps) / args.steps
+        result["decode_graph_replay"] = {"per_layer_us": round(ms_g * 1e3 / N_LAYERS, 2),
+                                         "GB/s": round(bytes_step / (ms_g * 1e-3) / 1e9, 1)}
+        del graph
 
     if not args.no_verify:
         # MTP verify: n_q = 2 with the causal mask across the two rows.
