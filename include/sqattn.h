@@ -136,6 +136,12 @@ int sqa_rope_norm_set_rows_q4_0(const sqa_tensor *dst, const sqa_tensor *src, co
 int sqa_rope_norm_f32(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w, float eps,
                       const sqa_tensor *pos, const sqa_rope *rope, void *stream);
 
+/* Support query for both producer forms (idx != NULL: the q4_0 one, else the
+ * F32 one), mirroring ggml_backend_supports_op (reference: src/backend/ffi.rs:
+ * 361-362). Returns 1 if the call with these operands would run. */
+int sqa_supports_rope_norm(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w,
+                           const sqa_tensor *pos, const sqa_rope *rope, const sqa_tensor *idx);
+
 /* ------------------------------------------------------------------------ */
 /* flash_attn_ext                                                            */
 /* ------------------------------------------------------------------------ */

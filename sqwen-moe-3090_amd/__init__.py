@@ -110,6 +110,7 @@ def lib():
             "sqa_supports_set_rows": (ctypes.c_int, [P, P, P]),
             "sqa_rope_norm_set_rows_q4_0": (ctypes.c_int, [P, P, P, f32, P, ctypes.POINTER(Rope), P, vp]),
             "sqa_rope_norm_f32": (ctypes.c_int, [P, P, P, f32, P, ctypes.POINTER(Rope), vp]),
+            "sqa_supports_rope_norm": (ctypes.c_int, [P, P, P, P, ctypes.POINTER(Rope), P]),
             "sqa_flash_attn_ext": (ctypes.c_int, [P, P, P, P, f32, f32, f32, P, vp, sz, vp]),
             "sqa_flash_attn_ext_workspace_size": (sz, [P, P, P, P]),
             "sqa_supports_flash_attn_ext": (ctypes.c_int, [P, P, P, P, f32, f32, f32, P]),

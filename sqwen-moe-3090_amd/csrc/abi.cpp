@@ -213,9 +213,8 @@ static int check_producer(const sqa_tensor *src, const sqa_tensor *norm_w, const
     return SQA_OK;
 }
 
-int sqa_rope_norm_set_rows_q4_0(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w,
-                                float eps, const sqa_tensor *pos, const sqa_rope *rope,
-                                const sqa_tensor *idx, void *stream) {
+static int check_producer_q4(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w,
+                             const sqa_tensor *pos, const sqa_rope *rope, const sqa_tensor *idx) {
     const char *what = "rope_norm_set_rows_q4_0";
     int st = check_producer(src, norm_w, pos, rope, what);
     if (st != SQA_OK) return st;
@@ -228,6 +227,25 @@ int sqa_rope_norm_set_rows_q4_0(const sqa_tensor *dst, const sqa_tensor *src, co
     if (dst->nb[0] != SQA_Q4_0_BLOCK_BYTES || dst->nb[1] % 2 || (uintptr_t)dst->data % 2 || idx->nb[0] % 8)
         return set_error(SQA_ERR_UNSUPPORTED, "%s: dst/idx strides not supported", what);
     if (n_tok > 0 && (!dst->data || !idx->data)) return set_error(SQA_ERR_INVALID, "%s: null data pointer", what);
+    return SQA_OK;
+}
+
+int sqa_supports_rope_norm(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w,
+                           const sqa_tensor *pos, const sqa_rope *rope, const sqa_tensor *idx) {
+    if (idx) return check_producer_q4(dst, src, norm_w, pos, rope, idx) == SQA_OK;
+    if (check_producer(src, norm_w, pos, rope, "rope_norm_f32") != SQA_OK) return 0;
+    if (!dst || dst->type != SQA_TYPE_F32 || dst->ne[0] != src->ne[0] || dst->ne[1] != src->ne[1] ||
+        dst->ne[2] != src->ne[2] || dst->nb[0] != 4 || dst->nb[1] != (uint64_t)(4 * src->ne[0]) ||
+        dst->nb[2] != (uint64_t)(4 * src->ne[0] * src->ne[1]) || (uintptr_t)dst->data % 16)
+        return 0;
+    return 1;
+}
+
+int sqa_rope_norm_set_rows_q4_0(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w,
+                                float eps, const sqa_tensor *pos, const sqa_rope *rope,
+                                const sqa_tensor *idx, void *stream) {
+    const int st = check_producer_q4(dst, src, norm_w, pos, rope, idx);
+    if (st != SQA_OK) return st;
     const float ts = powf(rope->freq_base, -2.0f / (float)rope->n_rot);
     return launch_rope_norm(dst, *src, norm_w, eps, *pos, *rope, ts, idx, (hipStream_t)stream);
 }

@@ -170,3 +170,9 @@ def test_producer_argument_checks_before_any_launch(sqa):
     assert call(good, ww=T(0, [D], [4], 8196)) == 1                     # unaligned weight
     out = T(0, [D, n_head, n_tok], [4, D * 4, n_head * D * 4], 65536)
     assert L.sqa_rope_norm_f32(by(out), by(src), by(w), 1e-6, by(pos), by(yarn), None) == 2
+    # the support query answers without launching, for both forms
+    assert L.sqa_supports_rope_norm(by(dst), by(src), by(w), by(pos), by(good), by(idx)) == 1
+    assert L.sqa_supports_rope_norm(by(dst), by(src), by(w), by(pos), by(yarn), by(idx)) == 0
+    assert L.sqa_supports_rope_norm(by(out), by(src), None, by(pos), by(good), None) == 1
+    assert L.sqa_supports_rope_norm(by(out), by(src), by(w), by(pos), by(sqa.rope_params(12, (3, 3, 0, 0), 1e7)),
+                                    None) == 0
