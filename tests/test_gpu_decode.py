@@ -58,6 +58,25 @@ def test_verify_two_rows_causal(sqa, orc, dev, n_kv):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("H,n_q,n_kv", [(8, 4, 3000), (4, 3, 1500), (2, 4, 700), (32, 1, 2500), (6, 2, 999)])
+def test_decode_kernel_other_group_sizes(sqa, orc, dev, H, n_q, n_kv):
+    """Two KV heads, G = H/2 query heads each, up to 4 positions and 16 rows per
+    KV head: the decode kernel's other shapes (4 positions fill its mask rows,
+    G = 16 at one position fills both row sets, G = 3 leaves rows ragged)."""
+    q, kq, vq = qkv(orc, 31 + H + n_q, n_q, n_kv, H=H, Hkv=2)
+    mask = orc.causal_mask(n_q, n_kv, n_kv - n_q)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    sqa.profile_begin(16)
+    try:
+        got = run_gpu(sqa, dev, q, kq, vq, mask)
+    finally:
+        sqa.profile_end()
+    assert sqa.profile_get("fa_decode")[1] == 1, "expected the decode kernel for this shape"
+    err = rel_err(got, ref)
+    print(f"decode H={H} n_q={n_q} n_kv={n_kv}: max err / rms = {err:.3e}")
+    assert err <= TOL
+
+
 def test_finite_mask_values_and_fully_masked_row(sqa, orc, dev):
     q, kq, vq = qkv(orc, 11, 2, 700)
     rng = np.random.default_rng(12)
