@@ -47,6 +47,8 @@
 // MFMA operand layouts (lane = 16*g + n):
 //   16x16x64 i8 : A[n][16g..16g+15]  B[16g..16g+15][n]  C[4g..4g+3][n]
 //   16x16x32 f16: A[n][8g..8g+7]     B[8g..8g+7][n]     C[4g..4g+3][n]
+#include <atomic>
+
 #include "common.hpp"
 
 namespace sqa {
@@ -783,15 +785,15 @@ int launch_fa_decode(const FaArgs &a, hipStream_t s) {
             p.mask_len = len8;
         }
     }
-    static bool lds_ok = false;
-    if (!lds_ok) {
+    static std::atomic<bool> lds_ok{false};  // set once per process; a repeated set is harmless
+    if (!lds_ok.load(std::memory_order_acquire)) {
         hipError_t e = hipFuncSetAttribute((const void *)fa_decode_kernel<false>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void *)fa_decode_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                     kLdsBytes);
         if (e != hipSuccess) return hip_status(e, "fa_decode LDS attribute");
-        lds_ok = true;
+        lds_ok.store(true, std::memory_order_release);
     }
     const int prof = profile_start("fa_decode", s);
     if (p.rows <= 8)

@@ -49,6 +49,8 @@
 //
 // Operand layout of the 16x16x32 MFMAs (64 lanes, lane = 16*g + n):
 //   A: A[row n][k = 8g..8g+7]   B: B[k = 8g..8g+7][col n]   C: C[rows 4g..4g+3][col n]
+#include <atomic>
+
 #include "common.hpp"
 
 namespace sqa {
@@ -812,12 +814,14 @@ int launch_fa_prefill(const FaArgs &a, hipStream_t s) {
     p.gate_nb2 = a.gate ? (int64_t)a.gate->nb[2] : 0;
 
     const int lds_bytes = kLdsMask + (p.mask ? 2 * pl.mask_stage : 0);
-    static int lds_set = 0;
-    if (lds_bytes > lds_set) {
+    static std::atomic<int> lds_set{0};  // largest size set so far; a repeated set is harmless
+    if (lds_bytes > lds_set.load(std::memory_order_acquire)) {
         e = hipFuncSetAttribute((const void *)fa_prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 lds_bytes);
         if (e != hipSuccess) return hip_status(e, "fa_prefill LDS attribute");
-        lds_set = lds_bytes;
+        int cur = lds_set.load(std::memory_order_relaxed);
+        while (cur < lds_bytes && !lds_set.compare_exchange_weak(cur, lds_bytes, std::memory_order_release)) {
+        }
     }
     prof = profile_start("fa_prefill", s);
     fa_prefill_kernel<<<dim3((unsigned)(pl.q_tiles * Hkv * pl.n_splits)), dim3(kThreads), lds_bytes, s>>>(p);
