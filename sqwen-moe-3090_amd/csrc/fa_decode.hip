@@ -91,7 +91,7 @@ constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kSlack = 8.0f;  // log2 of the largest P the lazy rescale admits
 static_assert(kTensorBytes % 1024 == 0, "a tile tensor must be whole DMA instructions");
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
-static_assert(32 * 1024 <= (kVStages - 1) * kTensorBytes, "Q staging must fit in V stages 1..2");
+static_assert(2 * 4 * 2 * 64 * 32 <= (kVStages - 1) * kTensorBytes, "Q operands must fit in V stages 1..2");
 
 // 16 bytes per lane from sbase + voff into LDS at m0 + 16 * lane. The data
 // arrives asynchronously; the caller waits with s_waitcnt vmcnt.
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
     if (p.q_pos0 >= 0 && k1 > p.q_pos0 + p.n_q) k1 = p.q_pos0 + p.n_q;  // no row sees past this
     const int n_tiles = k1 > k0 ? (int)((k1 - k0 + kTileKeys - 1) / kTileKeys) : 0;
 
-    uint8_t *qs_lds = smem + kOffV + kTensorBytes;  // Q rows, then Q operands (V stages 1-2)
+    uint8_t *qs_lds = smem + kOffV + kTensorBytes;  // Q operands (V stages 1-2, free until V(1) is issued)
     // Per-tile exchange areas
     _Float16 *pbuf = reinterpret_cast<_Float16 *>(smem + kOffP);
     float *mbuf = reinterpret_cast<float *>(smem + kOffM);
@@ -208,13 +208,12 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
 
     if (score) {
         // ============ score wavefronts: QK and softmax weights =================
-        wait_vm_barrier(0);  // Q rows landed (issued by the value wavefronts)
         // Q -> q8_0 block-diagonal B operands. Column n of C: row r = (n & 7)
         // [+ 8 for the second set], block 2*pair + (n >> 3). Lane (g, n) supplies
         // k = 16g..16g+15, i.e. values 16*(g&1).. of the column's block when
         // (g >> 1) == (n >> 3), zeros otherwise. The four wavefronts of a KV head
-        // each quantise one block pair (pair = wq) and exchange the operands
-        // through LDS (where the Q rows were).
+        // each load their block pair (pair = wq) of the Q rows straight from global
+        // memory at entry, quantise it and exchange the operands through LDS.
         constexpr int kSets = TWO ? 2 : 1;
         constexpr int kOpndBytes = 32;  // per lane: 16 code bytes, d_q, -8*sum(q8)
         int32x4 bq[kSets][4];
@@ -232,7 +231,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                 const bool row_ok = r < p.rows;
                 const int t = r / p.G;
                 const int hq = kvh * p.G + (r - t * p.G);
-                const float *qrow = reinterpret_cast<const float *>(qs_lds + (row_ok ? (t * p.H + hq) : 0) * 1024);
+                const float *qrow = reinterpret_cast<const float *>(p.q + (row_ok ? t * p.q_nb1 + hq * p.q_nb2 : 0));
                 const int blk = 2 * pr + (n >> 3);
                 float x[16];
 #pragma unroll
@@ -275,7 +274,6 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                 my_dq[set] = q_active ? dqv : dq2;
                 my_ci[set] = q_active ? civ : ci2;
             }
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every Q row read
 #pragma unroll
             for (int set = 0; set < kSets; ++set) {
                 uint8_t *o = qs_lds + (((kvh * 4 + pr) * kSets + set) * 64 + lane) * kOpndBytes;
@@ -529,17 +527,10 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             return (t + 2 < n_tiles ? per_k : 0) + (t < n_tiles ? per_v : 0);
         };
 
-        // ---------------- Q rows to LDS, then K 0-2 and V 0 ---------------------
-        const int q_rows = p.n_q * p.H;
-        for (int r = vw; r < q_rows; r += kValueWaves) {
-            const int t = r / p.H, h = r - t * p.H;
-            dma16(16u * lane, p.q + t * p.q_nb1 + h * p.q_nb2, lds0 + kOffV + kTensorBytes + 1024u * r);
-        }
+        // ---------------- K 0-2 and V 0 ------------------------------------------
         const int pre = n_tiles < kKStages - 1 ? n_tiles : kKStages - 1;
         for (int t = 0; t < pre; ++t) issue_k(t);
         if (n_tiles > 0) issue_v(0, 0);
-        wait_vm_barrier(per_k * pre + (n_tiles > 0 ? per_v : 0));           // Q landed (tiles may still be in flight)
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // Q rows read
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // Q operands published
         const int dq = wq;  // dims 64dq..64dq+63: blocks 2dq, 2dq+1
         // Nibble -> exact fp16 integer: the low nibble in mantissa bits 0-3 under
