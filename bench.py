@@ -276,7 +276,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of this single-GPU path; --gpus {args.gpus} is not "
-              "supported (multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+              "supported: the path runs on one GPU and has no multi-GPU mode", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
