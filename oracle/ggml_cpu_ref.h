@@ -1,7 +1,7 @@
 /*
  * ggml_cpu_ref.h - CPU oracle for the full-attention hot path.
  *
- * TEST INFRASTRUCTURE ONLY. This is the checker the HIP kernels are compared
+ * TEST INFRASTRUCTURE ONLY. This is the reference the HIP kernels are compared
  * against: only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline
  * leg may load it. The product library never links or calls it.
  *
