@@ -84,6 +84,56 @@ def time_steps(torch, fn, steps):
     return a.elapsed_time(b)  # ms
 
 
+def verify_leg(sqa, torch, dev, ks, vs, steps):
+    """MTP verify (n_q = 2: the current token plus one draft, causal across the
+    two rows) against plain decode (n_q = 1) over the first n_kv rows of the 10
+    layers' caches, at 32768, 131072 and 172032 keys. The two step kinds
+    alternate within one loop, each bracketed by its own events, so the
+    marginal cost of the draft row is a difference of neighbouring steps."""
+    out = {}
+    for n_kv in (32768, 131072, N_KV):
+        q1 = torch.randn((1, H, D), device=dev)
+        q2 = torch.randn((2, H, D), device=dev)
+        m1 = torch.empty((1, n_kv), dtype=torch.float16, device=dev)
+        m2 = torch.empty((2, n_kv), dtype=torch.float16, device=dev)
+        sqa.fill_causal_mask(m1, n_kv - 1)
+        sqa.fill_causal_mask(m2, n_kv - 2)
+        o1 = torch.empty((1, H, D), device=dev)
+        o2 = torch.empty((2, H, D), device=dev)
+        w1 = torch.empty(sqa.flash_attn_workspace_size(q1, ks[0], n_kv), dtype=torch.uint8, device=dev)
+        w2 = torch.empty(sqa.flash_attn_workspace_size(q2, ks[0], n_kv), dtype=torch.uint8, device=dev)
+
+        def run(q, m, o, w):
+            for li in range(N_LAYERS):
+                sqa.flash_attn_ext(q, ks[li], vs[li], n_kv, mask=m, out=o, workspace=w)
+
+        for _ in range(3):
+            run(q1, m1, o1, w1)
+            run(q2, m2, o2, w2)
+        rounds = max(10, steps)
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(rounds)]
+        torch.cuda.synchronize()
+        for r in range(rounds):
+            ev[r][0].record()
+            run(q1, m1, o1, w1)
+            ev[r][1].record()
+            run(q2, m2, o2, w2)
+            ev[r][2].record()
+        torch.cuda.synchronize()
+        t1 = sorted(e[0].elapsed_time(e[1]) for e in ev)
+        t2 = sorted(e[1].elapsed_time(e[2]) for e in ev)
+        marg = sorted(e[1].elapsed_time(e[2]) / e[0].elapsed_time(e[1]) - 1 for e in ev)
+        med = lambda xs: xs[len(xs) // 2]
+        out[f"n_kv_{n_kv}"] = {
+            "nq1_per_layer_us": round(med(t1) * 1e3 / N_LAYERS, 2),
+            "nq2_per_layer_us": round(med(t2) * 1e3 / N_LAYERS, 2),
+            "nq2_GB/s": round(N_LAYERS * layer_bytes(n_kv, 2) / (med(t2) * 1e-3) / 1e9, 1),
+            "draft_row_marginal_pct": round(100 * med(marg), 1),
+            "marginal_pct_iqr": [round(100 * marg[len(marg) // 4], 1), round(100 * marg[3 * len(marg) // 4], 1)],
+            "rounds": rounds}
+    return out
+
+
 def prefill_flops(n_q, start, heads=H, head_dim=D):
     """QK^T + PV multiply-adds (2 flops each) over the visible keys."""
     keys = n_q * (start + 1) + n_q * (n_q - 1) // 2
@@ -243,9 +293,33 @@ def producer_leg(sqa, torch, dev, steps, warmup):
     return out
 
 
+def host_cpu():
+    """(CPU model, logical CPUs usable by this process)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return model, n
+
+
+def cpu_threads(rows):
+    """Threads for the oracle: one (query, head) row per task as ggml partitions
+    its FA work, capped at the 16 host cores a one-GPU share of the box holds."""
+    return max(1, min(host_cpu()[1], 16, rows))
+
+
 def cpu_baseline(orc, kq, vq, q, mask, budget_s=8.0):
     """The oracle (C restatement of ggml's CPU flash_attn_ext) on this host."""
-    threads = min(os.cpu_count() or 1, 16, q.shape[0] * q.shape[1])
+    threads = cpu_threads(q.shape[0] * q.shape[1])
     orc.flash_attn_ext(q, kq, vq, mask, threads=threads)  # warm
     t0 = time.perf_counter()
     reps = 0
@@ -256,6 +330,37 @@ def cpu_baseline(orc, kq, vq, q, mask, budget_s=8.0):
             break
     dt = (time.perf_counter() - t0) / reps
     return dt, threads, reps
+
+
+def cpu_prefill_baseline(orc, np, n_pos=16, seed=11):
+    """The oracle on a bounded sample of the pp512 workload: n_pos of the 512
+    query positions (evenly spaced, all 16 heads) over the 16896-key cache with
+    their causal mask rows, timed and scaled by the visible keys of all 512
+    positions over those of the sample."""
+    n_kv = PP_START + PP_N_Q
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((n_kv, HKV * D), dtype=np.float32)
+    v = rng.standard_normal((n_kv, HKV * D), dtype=np.float32)
+    kq = orc.quantize_q4_0(k).reshape(n_kv, HKV, -1)
+    vq = orc.quantize_q4_0(v).reshape(n_kv, HKV, -1)
+    pos = np.linspace(0, PP_N_Q - 1, n_pos).astype(np.int64)
+    q = rng.standard_normal((n_pos, H, D), dtype=np.float32)
+    mask = orc.causal_mask(PP_N_Q, n_kv, PP_START)[pos]
+    threads = cpu_threads(n_pos * H)
+    orc.flash_attn_ext(q, kq, vq, mask, threads=threads)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while reps < 3:
+        orc.flash_attn_ext(q, kq, vq, mask, threads=threads)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    sample_keys = int(sum(PP_START + p + 1 for p in pos))
+    full_keys = PP_N_Q * (PP_START + 1) + PP_N_Q * (PP_N_Q - 1) // 2
+    layer_s = dt * full_keys / sample_keys
+    return {"value": round(prefill_flops(PP_N_Q, PP_START) / layer_s / 1e12, 5), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": f"{n_pos} of the 512 pp512 query positions x 16 heads over {n_kv} keys with their "
+                      f"causal mask rows, {reps} runs of {dt * 1e3:.1f} ms, scaled by visible keys to "
+                      f"{layer_s * 1e3:.0f} ms per layer"}
 
 
 def main():
@@ -361,23 +466,7 @@ def main():
         del graph
 
     if not args.no_verify:
-        # MTP verify: n_q = 2 with the causal mask across the two rows.
-        q2 = torch.randn((2, H, D), device=dev, dtype=torch.float32)
-        m2 = torch.empty((2, N_KV), dtype=torch.float16, device=dev)
-        sqa.fill_causal_mask(m2, N_KV - 2)
-        o2 = torch.empty((2, H, D), dtype=torch.float32, device=dev)
-        ws2 = torch.empty(sqa.flash_attn_workspace_size(q2, ks[0], N_KV), dtype=torch.uint8, device=dev)
-
-        def step2():
-            for li in range(N_LAYERS):
-                sqa.flash_attn_ext(q2, ks[li], vs[li], N_KV, mask=m2, out=o2, workspace=ws2)
-
-        for _ in range(2):
-            step2()
-        ms2 = time_steps(torch, step2, args.steps) / args.steps
-        result["verify_nq2"] = {"per_layer_us": round(ms2 * 1e3 / N_LAYERS, 2),
-                                "GB/s": round(N_LAYERS * layer_bytes(N_KV, 2) / (ms2 * 1e-3) / 1e9, 1),
-                                "draft_row_marginal_pct": round(100 * (ms2 / ms_per_step - 1), 1)}
+        result["verify_nq2"] = verify_leg(sqa, torch, dev, ks, vs, args.steps)
 
     if not args.no_prefill:
         result["prefill_pp512"] = prefill_leg(sqa, torch, dev, max(2, args.steps // 2), 2)
@@ -397,10 +486,15 @@ def main():
         qh = qs[0].cpu().numpy()
         mh = mask.cpu().numpy()
         dt, threads, reps = cpu_baseline(orc, kq, vq, qh, mh)
+        model, ncpu = host_cpu()
         result["cpu_baseline"] = {"value": round(layer_bytes(N_KV, 1) / dt / 1e9, 3), "unit": "GB/s",
                                   "cores": threads, "kind": "port",
                                   "sample": f"{reps} runs of one 172032-key decode layer (n_q=1, 16 rows); "
-                                            f"{dt * 1e3:.1f} ms per layer"}
+                                            f"{dt * 1e3:.1f} ms per layer",
+                                  "host_cpu": model, "host_logical_cpus": ncpu,
+                                  "build": "gcc -O3 -march=x86-64-v3 -fopenmp, one (query, head) row per thread"}
+        if not args.no_prefill:
+            result["cpu_baseline_prefill_pp512"] = cpu_prefill_baseline(orc, np)
         # Check the timed GPU output of that layer against the oracle.
         o_gpu = sqa.flash_attn_ext(qs[0], ks[0], vs[0], N_KV, mask=mask).cpu().numpy()
         o_ref = orc.flash_attn_ext(qh, kq, vq, mh, threads=threads)

@@ -426,7 +426,28 @@ class KvCache:
         _check(lib().sqa_kv_cache_append(self._h, slot, ctypes.byref(tk), ctypes.byref(tv), ctypes.byref(ti),
                                          _stream(stream)))
 
+    def workspace_size(self, slot, q):
+        """Workspace bytes of attend() for q over the current [0, n_kv_padded) views."""
+        n_q, H, D = q.shape
+        tq, tk, tv = q_desc(q), self.view(slot, "k"), self.view(slot, "v")
+        to = Tensor.make(TYPE_F32, [D, H, n_q, 1], [4, D * 4, H * D * 4], 16)
+        return int(lib().sqa_flash_attn_ext_workspace_size(ctypes.byref(tq), ctypes.byref(tk), ctypes.byref(tv),
+                                                           ctypes.byref(to)))
+
     def attend(self, slot, q, mask=None, scale=None, out=None, workspace=None, stream=None):
-        """flash_attn_ext over this layer's [0, n_kv_padded) view (attn.rs:228-251)."""
-        return flash_attn_ext(q, self.k[slot], self.v[slot], self.n_kv_padded(), mask=mask, scale=scale,
-                              out=out, workspace=workspace, stream=stream)
+        """flash_attn_ext over this layer's [0, n_kv_padded) views, taken from the
+        library's k_view/v_view (the permuted views of kv.rs:401-447 that
+        attn.rs:228-251 hands to ggml_flash_attn_ext)."""
+        n_q, H, D = q.shape
+        scale = D ** -0.5 if scale is None else scale
+        if out is None:
+            out = torch.empty((n_q, H, D), dtype=torch.float32, device=q.device)
+        tq, tk, tv = q_desc(q), self.view(slot, "k"), self.view(slot, "v")
+        to, tm = out_desc(out), mask_desc(mask)
+        if workspace is None:
+            workspace, _ = _workspace(self.workspace_size(slot, q), q.device)
+        wptr = workspace.data_ptr() if workspace is not None else None
+        wbytes = workspace.numel() if workspace is not None else 0
+        _check(lib().sqa_flash_attn_ext(ctypes.byref(tq), ctypes.byref(tk), ctypes.byref(tv), _ref(tm), scale,
+                                        0.0, 0.0, ctypes.byref(to), wptr, wbytes, _stream(stream)))
+        return out

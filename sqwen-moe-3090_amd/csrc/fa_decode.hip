@@ -40,14 +40,22 @@
 //     KV head reads the four maxima used, takes their maximum, and rescales its
 //     share (l, O, and the P values of that tile) onto it.
 //   * PV: v_mfma_f32_16x16x32_f16 with fp32 accumulation. P enters as an fp16
-//     hi + lo pair (~22 bits, two MFMAs); V is (nib - 8) * d_v (exact fp16
-//     integer 1024 + nib minus 1032, times d_v), rounded once to fp16.
+//     hi + lo pair (~22 bits); V = (nib - 8) * d_v (the code from the exact fp16
+//     integer 1024 + nib minus 1032) as an fp16 hi + lo pair that holds it
+//     exactly, so O += Ph Vh + Pl Vh + Ph Vl: three MFMAs, every product exact
+//     in fp32. A row that a few keys dominate then carries no fp16 rounding of
+//     V or P into its output (ggml's CPU path dequantizes V to fp32 exactly).
+//   * A key that no row of the call sees (masked in every row, past the split
+//     or past the cache end) contributes exactly 0 whatever its bytes, as in
+//     ggml's CPU loop, which skips masked keys: a -inf mask entry replaces the
+//     logit, and the score wavefronts publish which keys have P != 0 in some
+//     row, so the value wavefronts zero the others' V scales.
 //   * Splits are merged by fa_combine (fa_combine.hip).
 //
 // MFMA operand layouts (lane = 16*g + n):
 //   16x16x64 i8 : A[n][16g..16g+15]  B[16g..16g+15][n]  C[4g..4g+3][n]
 //   16x16x32 f16: A[n][8g..8g+7]     B[8g..8g+7][n]     C[4g..4g+3][n]
-#include <atomic>
+#include <mutex>
 
 #include "common.hpp"
 
@@ -320,7 +328,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             if (t > 0) {
                 const int pb = (t - 1) & 1;
                 const uint4 fl = *reinterpret_cast<const uint4 *>(fbuf + (pb * 2 + kvh) * 4);
-                if ((fl.x | fl.y | fl.z | fl.w) != 0) {
+                if ((fl.x | fl.y | fl.z | fl.w) & 1u) {
                     const float *mr = mbuf + (pb * 2 + kvh) * 64;
                     const float mn = fmaxf(fmaxf(mr[my_r], mr[16 + my_r]), fmaxf(mr[32 + my_r], mr[48 + my_r]));
                     l_acc = l_acc * exp2_or_zero(m_ref, mn) + l_prev * exp2_or_zero(m_used, mn);
@@ -402,7 +410,9 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                     const uint16_t mb = mrow[i];
                     _Float16 mh;
                     __builtin_memcpy(&mh, &mb, 2);
-                    s[i] = fmaf((float)mh, kLog2e, s[i]);
+                    // a -inf entry excludes the key whatever its logit (even NaN from a
+                    // garbage scale): ggml's CPU loop skips such keys
+                    s[i] = mb == 0xFC00u ? -INFINITY : fmaf((float)mh, kLog2e, s[i]);
                 }
             }
             if (tail) {
@@ -450,7 +460,15 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                 *reinterpret_cast<half4 *>(prow + 64) = pl;
                 if (g == 0) mbuf[((buf * 2 + kvh) * 4 + wq) * 16 + my_r] = mu;
             }
-            if (lane == 0) fbuf[(buf * 2 + kvh) * 4 + wq] = need ? 1u : 0u;
+            // keys of this wavefront that some row sees: bit 4g + i of the 16
+            uint32_t alive16 = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint64_t b = __ballot(pv[i] != 0.0f);  // bit 16g + n: row n, key 4g + i
+#pragma unroll
+                for (int gg = 0; gg < 4; ++gg) alive16 |= ((b >> (16 * gg)) & 0xFFFFu) ? 1u << (4 * gg + i) : 0u;
+            }
+            if (lane == 0) fbuf[(buf * 2 + kvh) * 4 + wq] = (need ? 1u : 0u) | (alive16 << 16);
         }
 
         // ---------------- this split's softmax statistics ------------------------
@@ -601,14 +619,21 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                         }
                     }
 
+            // flags of the score wavefronts: bit 0 = maximum moved, bits 16-31 = their
+            // 16 keys that some row of the call can see (P != 0)
+            const uint4 fl = *reinterpret_cast<const uint4 *>(fbuf + (pb * 2 + kvh) * 4);
+
             // -- d_v of the slice's two blocks for all 64 keys, in B k-slot order --
+            // A key no row sees (masked, past the range or past the cache end) gets
+            // d_v = 0, so its bytes, whatever they hold, add exactly 0 as ggml's CPU
+            // loop skips such keys.
             {
                 const uint8_t *src = smem + sv_off + csrc;
                 uint32_t da = lds16(src), db = lds16(src + kLdsRow);
-                if (kt + kTileKeys > k1) {  // rows past the range may hold any bytes: zero scales keep P*V finite
-                    da = kt + ckey < k1 ? da : 0u;
-                    db = kt + ckey + 1 < k1 ? db : 0u;
-                }
+                const uint64_t alive = (uint64_t)((fl.x >> 16) | (fl.y & 0xFFFF0000u)) |
+                                       ((uint64_t)((fl.z >> 16) | (fl.w & 0xFFFF0000u)) << 32);
+                da = (alive >> ckey) & 1 ? da : 0u;
+                db = (alive >> (ckey + 1)) & 1 ? db : 0u;
                 *reinterpret_cast<uint32_t *>(dv_comp + cdst) = da | (db << 16);
             }
 
@@ -619,8 +644,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             pa[1] = *reinterpret_cast<const half8 *>(prow + 32);
             pl[0] = *reinterpret_cast<const half8 *>(prow + 64);
             pl[1] = *reinterpret_cast<const half8 *>(prow + 96);
-            const uint4 fl = *reinterpret_cast<const uint4 *>(fbuf + (pb * 2 + kvh) * 4);
-            if ((fl.x | fl.y | fl.z | fl.w) != 0) {
+            if ((fl.x | fl.y | fl.z | fl.w) & 1u) {
                 const float *mr = mbuf + (pb * 2 + kvh) * 64;
                 float fac[4];
 #pragma unroll
@@ -650,13 +674,17 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             }
 
             // -- O += P V over the two halves of the tile and the slice's blocks ---
+            // V = (nib - 8) * d_v exactly, as Vh + Vl: Vh = fp16(V) and Vl = V - Vh by
+            // one fma. A code has at most 3 significant bits and d_v 11, so V has at
+            // most 14 and the residual at most 3: both halves are exact in fp16. With
+            // P as hi + lo, O += Ph Vh + Pl Vh + Ph Vl (Pl Vl is below 2^-22 of PV).
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
 #pragma unroll
                 for (int bl = 0; bl < 2; ++bl) {
                     const uint4 dv4 = *reinterpret_cast<const uint4 *>(dv_comp + ((bl * 2 + h) * 4 + g) * 16);
                     const uint32_t dvw[4] = {dv4.x, dv4.y, dv4.z, dv4.w};
-                    half8 blo, bhi;
+                    half8 blo, bhi, blo_r, bhi_r;
 #pragma unroll
                     for (int m = 0; m < 4; ++m) {
                         const uint32_t xm = x[4 * (2 * h + bl) + m];
@@ -666,17 +694,26 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                         __builtin_memcpy(&lo, &lw, 4);
                         __builtin_memcpy(&hi, &hw, 4);
                         __builtin_memcpy(&dv2, &dvw[m], 4);
-                        lo = (lo + off_lo) * dv2;  // (nib - 8) * d_v
-                        hi = (hi + off_hi) * dv2;
-                        blo[2 * m] = lo[0];
-                        blo[2 * m + 1] = lo[1];
-                        bhi[2 * m] = hi[0];
-                        bhi[2 * m + 1] = hi[1];
+                        lo = lo + off_lo;  // nib - 8, exact
+                        hi = hi + off_hi;
+                        const half2v lo_h = lo * dv2, hi_h = hi * dv2;
+                        const half2v lo_r = __builtin_elementwise_fma(lo, dv2, -lo_h);
+                        const half2v hi_r = __builtin_elementwise_fma(hi, dv2, -hi_h);
+                        blo[2 * m] = lo_h[0];
+                        blo[2 * m + 1] = lo_h[1];
+                        bhi[2 * m] = hi_h[0];
+                        bhi[2 * m + 1] = hi_h[1];
+                        blo_r[2 * m] = lo_r[0];
+                        blo_r[2 * m + 1] = lo_r[1];
+                        bhi_r[2 * m] = hi_r[0];
+                        bhi_r[2 * m + 1] = hi_r[1];
                     }
                     acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[h], blo, acc[2 * bl], 0, 0, 0);
                     acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[h], bhi, acc[2 * bl + 1], 0, 0, 0);
                     acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[h], blo, acc[2 * bl], 0, 0, 0);
                     acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[h], bhi, acc[2 * bl + 1], 0, 0, 0);
+                    acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[h], blo_r, acc[2 * bl], 0, 0, 0);
+                    acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[h], bhi_r, acc[2 * bl + 1], 0, 0, 0);
                 }
             }
         }
@@ -776,16 +813,16 @@ int launch_fa_decode(const FaArgs &a, hipStream_t s) {
             p.mask_len = len8;
         }
     }
-    static std::atomic<bool> lds_ok{false};  // set once per process; a repeated set is harmless
-    if (!lds_ok.load(std::memory_order_acquire)) {
-        hipError_t e = hipFuncSetAttribute((const void *)fa_decode_kernel<false>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void *)fa_decode_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    kLdsBytes);
-        if (e != hipSuccess) return hip_status(e, "fa_decode LDS attribute");
-        lds_ok.store(true, std::memory_order_release);
-    }
+    static std::once_flag lds_once;  // the LDS limit is raised once per process
+    static hipError_t lds_err = hipSuccess;
+    std::call_once(lds_once, [] {
+        lds_err = hipFuncSetAttribute((const void *)fa_decode_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      kLdsBytes);
+        if (lds_err == hipSuccess)
+            lds_err = hipFuncSetAttribute((const void *)fa_decode_kernel<true>,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    });
+    if (lds_err != hipSuccess) return hip_status(lds_err, "fa_decode LDS attribute");
     const int prof = profile_start("fa_decode", s);
     if (p.rows <= 8)
         fa_decode_kernel<false><<<dim3((unsigned)p.n_splits), dim3(kThreads), kLdsBytes, s>>>(p);

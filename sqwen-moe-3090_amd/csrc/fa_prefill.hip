@@ -27,11 +27,15 @@
 //     online softmax in fp32 (base 2, rescaled whenever a row maximum grows, so
 //     the largest P is exactly 1). P (fp32) and the rescale factors go to LDS.
 //   value wave 4 + w, the same 32 rows, holds their O (128 registers) one tile
-//     behind: O = alpha O + P V per block b with
-//     A = fp16(P 2^e d_v) (one rounding, the only one on the path) and B = the
-//     exact V codes. 2^e is one power of two per KV head that brings max |d_v|
-//     into [1, 2): it keeps A clear of fp16 subnormals and overflow, and
-//     cancels in O = PV / l because l is summed from the same scaled P.
+//     behind: O = alpha O + P V per block b with A = P 2^e d_v as an fp16
+//     hi + lo pair (two MFMAs, ~22 bits) and B = the exact V codes, so every
+//     product is exact in fp32. 2^e is one power of two per KV head that
+//     brings max |d_v| into [1, 2): it keeps A clear of fp16 subnormals and
+//     overflow, and cancels in O = PV / l because l is summed from the same
+//     scaled P.
+//   A masked key contributes exactly 0 even over bytes that are not valid q4_0
+//   (as ggml's CPU loop, which skips it): a -inf mask entry replaces the logit,
+//   P d_v is formed with 0 * x = 0, and NaN/Inf scales stay out of max |d_v|.
 // Computing S^T (keys as rows) leaves each lane with 8 logits of one query row
 // in the A-operand layout of the P*V MFMA. K rows sit in LDS in the order
 // r -> key sigma(r) = 8*((r>>2)&3) + 4*(r>>4) + (r&3), which makes a lane's 8
@@ -49,7 +53,7 @@
 //
 // Operand layout of the 16x16x32 MFMAs (64 lanes, lane = 16*g + n):
 //   A: A[row n][k = 8g..8g+7]   B: B[k = 8g..8g+7][col n]   C: C[rows 4g..4g+3][col n]
-#include <atomic>
+#include <mutex>
 
 #include "common.hpp"
 
@@ -84,7 +88,8 @@ constexpr int kLdsMask = kLdsA + 2 * kABuf;       // [qb positions][32 keys] f16
 constexpr float kLog2e = 1.4426950408889634f;
 
 static_assert(kTileBytes == 49664 && kTileBytes % 256 == 0, "tile record");
-static_assert(kLdsMask + 2 * 128 * kPK * 2 <= 160 * 1024, "LDS budget");
+constexpr int kLdsMaxBytes = kLdsMask + 2 * 128 * kPK * 2;  // with the mask stages of G = 1
+static_assert(kLdsMaxBytes <= 160 * 1024, "LDS budget");
 
 __device__ __forceinline__ float h2f(uint32_t bits) {
     const uint16_t b = (uint16_t)bits;
@@ -206,7 +211,9 @@ __global__ __launch_bounds__(256) void kvprep_kernel(const uint8_t *__restrict__
 #pragma unroll
             for (int kk = 0; kk < 32; ++kk) {
                 dd[kk] = *reinterpret_cast<const uint16_t *>(sv + kHeadRowBytes * (32 * u + kk) + 18 * b);
-                const uint32_t mag = dd[kk] & 0x7fffu;
+                // the largest finite |d_v| sets the power of two applied to P d_v; a
+                // NaN/Inf scale (bytes that are not q4_0) stays out of it
+                const uint32_t mag = (dd[kk] & 0x7C00u) == 0x7C00u ? 0u : (dd[kk] & 0x7fffu);
                 dmax = mag > dmax ? mag : dmax;
             }
             uint8_t *vrec = kv + ((int64_t)h * kv_tiles + ((k0 >> 5) + u)) * kTileBytes + kKHalf;
@@ -519,8 +526,12 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                 for (int rg = 0; rg < kRG; ++rg) {
                     const uint32_t mw[4] = {mrow[rg].x, mrow[rg].y, mrow[rg].z, mrow[rg].w};
 #pragma unroll
-                    for (int jj = 0; jj < 8; ++jj)
-                        s[rg][jj] = fmaf(h2f((mw[jj >> 1] >> (16 * (jj & 1))) & 0xffff), kLog2e, s[rg][jj]);
+                    for (int jj = 0; jj < 8; ++jj) {
+                        // a -inf entry excludes the key whatever its logit (even NaN from
+                        // a garbage scale): ggml's CPU loop skips such keys
+                        const uint32_t mb = (mw[jj >> 1] >> (16 * (jj & 1))) & 0xffff;
+                        s[rg][jj] = mb == 0xFC00u ? -INFINITY : fmaf(h2f(mb), kLog2e, s[rg][jj]);
+                    }
                 }
             }
             if (nvalid < kPK || (p.q_pos0 >= 0 && kt + kPK - 1 > p.q_pos0 + q_base)) {
@@ -622,21 +633,33 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                 const uint4 u = *reinterpret_cast<const uint4 *>(vs + kOffDv + 64 * b + 16 * g);
                 __builtin_memcpy(&dvb, &u, 16);
             }
-            half8 a[kRG];
+            // A = P 2^e d_v as an fp16 hi + lo pair (22 bits): the products with the
+            // exact V codes are then exact in fp32, so a row that a few keys
+            // dominate carries no fp16 rounding of P d_v into its output.
+            half8 bv[2];
 #pragma unroll
-            for (int rg = 0; rg < kRG; ++rg)
+            for (int hf = 0; hf < 2; ++hf) bv[hf] = lds_half8(smem, vb0 + 1024 * (2 * b + hf), vb1 + 1024 * (2 * b + hf));
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) a[rg][jj] = (_Float16)__builtin_fmaf(pf[rg][jj], (float)dvb[jj], 0.0f);
+            for (int rg = 0; rg < kRG; ++rg) {
+                half8 a, al;
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                const int T = 2 * b + hf;
-                const half8 bv = lds_half8(smem, vb0 + 1024 * T, vb1 + 1024 * T);
+                for (int jj = 0; jj < 8; ++jj) {
+                    // 0 * x = 0 for every x (v_mul_legacy): a key with P = 0 adds
+                    // exactly 0 whatever its V scale holds
+                    float x;
+                    asm("v_mul_legacy_f32 %0, %1, %2" : "=v"(x) : "v"(pf[rg][jj]), "v"((float)dvb[jj]));
+                    a[jj] = (_Float16)x;
+                    al[jj] = (_Float16)(x - (float)a[jj]);
+                }
                 // O = alpha O + P V; the product is applied unconditionally (exact
                 // for alpha = 1): a conditional rescale makes the compiler keep a
                 // second copy of O and spill
 #pragma unroll
-                for (int rg = 0; rg < kRG; ++rg)
-                    acc[rg][T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[rg], bv, acc[rg][T] * a4[rg], 0, 0, 0);
+                for (int hf = 0; hf < 2; ++hf) {
+                    const int T = 2 * b + hf;
+                    acc[rg][T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv[hf], acc[rg][T] * a4[rg], 0, 0, 0);
+                    acc[rg][T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv[hf], acc[rg][T], 0, 0, 0);
+                }
             }
         }
     }
@@ -814,15 +837,15 @@ int launch_fa_prefill(const FaArgs &a, hipStream_t s) {
     p.gate_nb2 = a.gate ? (int64_t)a.gate->nb[2] : 0;
 
     const int lds_bytes = kLdsMask + (p.mask ? 2 * pl.mask_stage : 0);
-    static std::atomic<int> lds_set{0};  // largest size set so far; a repeated set is harmless
-    if (lds_bytes > lds_set.load(std::memory_order_acquire)) {
-        e = hipFuncSetAttribute((const void *)fa_prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                lds_bytes);
-        if (e != hipSuccess) return hip_status(e, "fa_prefill LDS attribute");
-        int cur = lds_set.load(std::memory_order_relaxed);
-        while (cur < lds_bytes && !lds_set.compare_exchange_weak(cur, lds_bytes, std::memory_order_release)) {
-        }
-    }
+    // The function's LDS limit is raised once per process to the largest size
+    // any launch uses, so concurrent first calls cannot leave a smaller one set.
+    static std::once_flag lds_once;
+    static hipError_t lds_err = hipSuccess;
+    std::call_once(lds_once, [] {
+        lds_err = hipFuncSetAttribute((const void *)fa_prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      kLdsMaxBytes);
+    });
+    if (lds_err != hipSuccess) return hip_status(lds_err, "fa_prefill LDS attribute");
     prof = profile_start("fa_prefill", s);
     fa_prefill_kernel<<<dim3((unsigned)(pl.q_tiles * Hkv * pl.n_splits)), dim3(kThreads), lds_bytes, s>>>(p);
     profile_stop(prof, s);

@@ -121,3 +121,39 @@ def test_full_size_against_oracle(sqa, orc, dev, n_q, n_kv):
     err = rel_err(got, ref)
     print(f"n_q={n_q} n_kv={n_kv}: max err / rms = {err:.3e}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("n_kv", [1, 2, 17, 40])
+def test_few_visible_keys_with_outliers(sqa, orc, dev, n_kv):
+    """A row that a few keys dominate: its output is a handful of V rows, so an
+    fp16 rounding of V or P would show at full size (1% of the channels x8)."""
+    q, kq, vq = qkv(orc, 300 + n_kv, 2, n_kv, outliers=5)
+    mask = orc.causal_mask(2, n_kv, max(n_kv - 2, 0))
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    err = rel_err(got, ref)
+    print(f"decode n_kv={n_kv} outliers: max err / rms = {err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("n_q", [1, 2])
+def test_masked_rows_with_garbage_bytes(sqa, orc, dev, n_q):
+    """Masked cache rows are never read by ggml's CPU loop; here they hold 0xFF
+    bytes (NaN block scales) or random bytes (any scale, finite or not, up to
+    65504), and must not change the output."""
+    n_kv = 1000
+    q, kq, vq = qkv(orc, 41 + n_q, n_q, n_kv)
+    rng = np.random.default_rng(42)
+    dead = rng.choice(n_kv - 2, 300, replace=False)
+    kq, vq = kq.copy(), vq.copy()
+    kq[dead[:150]] = 0xFF
+    vq[dead[:150]] = 0xFF
+    kq[dead[150:]] = rng.integers(0, 256, kq[dead[150:]].shape, dtype=np.uint8)
+    vq[dead[150:]] = rng.integers(0, 256, vq[dead[150:]].shape, dtype=np.uint8)
+    mask = orc.causal_mask(n_q, n_kv, n_kv - n_q)
+    mask[:, dead] = -np.inf
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    assert np.all(np.isfinite(ref))
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    assert np.all(np.isfinite(got))
+    assert rel_err(got, ref) <= TOL

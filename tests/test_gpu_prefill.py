@@ -90,3 +90,40 @@ def test_small_chunks_outside_the_decode_kernel(sqa, orc, dev, H, Hkv, n_q):
     ref = orc.flash_attn_ext(q, kq, vq, mask)
     got = run_gpu(sqa, dev, q, kq, vq, mask)
     assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("n_q,n_kv,start", [(64, 64, 0), (300, 512, 0), (494, 512, 17)])
+def test_chunk_at_context_start_with_outliers(sqa, orc, dev, n_q, n_kv, start):
+    """The first ubatch of a prompt: early rows see a few keys, so their outputs
+    are a handful of V rows at full size next to rows averaging hundreds of
+    keys (1% of the channels x8): an fp16 rounding of P d_v would show."""
+    q, kq, vq = qkv(orc, 500 + n_q, n_q, n_kv, outliers=5)
+    mask = orc.causal_mask(n_q, n_kv, start)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    err = rel_err(got, ref)
+    print(f"prefill chunk n_q={n_q} start={start} outliers: max err / rms = {err:.3e}")
+    assert err <= TOL
+
+
+def test_prefill_masked_rows_with_garbage_bytes(sqa, orc, dev):
+    """Masked cache rows holding 0xFF bytes (NaN block scales, what an unzeroed
+    buffer may hold) or stale rows of other data (a rewound draft) do not change
+    the output (ggml's CPU loop never reads them)."""
+    n_q, n_kv = 40, 1200
+    q, kq, vq = qkv(orc, 43, n_q, n_kv)
+    rng = np.random.default_rng(44)
+    dead = rng.choice(n_kv - n_q, 400, replace=False)
+    _, k_old, v_old = qkv(orc, 45, 1, len(dead) - 200)
+    kq, vq = kq.copy(), vq.copy()
+    kq[dead[:200]] = 0xFF
+    vq[dead[:200]] = 0xFF
+    kq[dead[200:]] = k_old
+    vq[dead[200:]] = v_old
+    mask = orc.causal_mask(n_q, n_kv, n_kv - n_q)
+    mask[:, dead] = -np.inf
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    assert np.all(np.isfinite(ref))
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    assert np.all(np.isfinite(got))
+    assert rel_err(got, ref) <= TOL
