@@ -6,22 +6,28 @@
 // the reference for n_q = 1..2 (decode step, MTP verify of runner.rs:1263-1270).
 //
 // Work split
-//   A workgroup (16 wavefronts, one per CU) owns a contiguous key range (a
-//   "split") for both KV heads and walks it in 64-key tiles. Eight score
-//   wavefronts (KV head w >> 2, 16-key quarter w & 3 of every tile) compute the
-//   logits and the softmax weights P of tile t; eight value wavefronts (KV head
-//   v >> 2, 64-dim slice v & 3 of the output) accumulate P V of tile t-1 over
+//   The key range is cut into one split per CU. Each split is served by two
+//   workgroups, one per KV head, that the dispatcher places on the same XCD
+//   (so the cache lines the two heads share in a 288-byte row are fetched from
+//   HBM once and served to the second workgroup by that XCD's L2); two such
+//   workgroups fit on a CU, so one head's wavefronts can issue while the
+//   other's wait at their barrier. A workgroup (8 wavefronts) walks its split
+//   in 64-key tiles: four score wavefronts (16-key quarter w of every tile)
+//   compute the logits and the softmax weights P of tile t; four value
+//   wavefronts (64-dim slice v of the output) accumulate P V of tile t-1 over
 //   all 64 keys of that tile. P crosses from score to value wavefronts through
-//   LDS, one tile behind, so one barrier per tile serves both. A value wavefront
-//   owns its output dims outright: there is no cross-wavefront merge of O.
+//   LDS, one tile behind, so one barrier per tile serves both. A value
+//   wavefront owns its output dims outright: there is no merge of O.
 //
 // Memory pipeline
 //   Tiles move from HBM to LDS with global_load_lds_dwordx4 (16 bytes per lane,
-//   no registers): K (and the tile's F16 mask rows) into a ring of 4 stages,
-//   issued 3 tiles ahead of the QK that reads them; V into a ring of 3 stages,
-//   issued 2 tiles ahead of the PV that reads them. Each 288-byte cache row
-//   lands in a 304-byte LDS row (a duplicate chunk is fetched into the pad) so
-//   that neighbouring rows start on different banks.
+//   no registers): the head's 144 bytes of each 288-byte cache row land in a
+//   160-byte LDS row (nine data chunks and a pad chunk). K (and the tile's F16
+//   mask rows) go into a ring of 3 stages, issued 2 tiles ahead of the QK that
+//   reads them; V into a ring of 3 stages, issued 1 tile ahead of its tile's QK,
+//   i.e. 2 ahead of the PV that reads it. LDS rows rotate their chunks so that
+//   the rows a wavefront reads together sit on different banks: K rows 8-15 of
+//   each 16-row group by one chunk, V rows by two chunks per 8-row group.
 //
 // Arithmetic (ggml's CPU flash_attn_ext within fp32 rounding)
 //   * QK: Q is rounded to q8_0 per 32-value block as ggml's x86 from_float does
@@ -37,14 +43,17 @@
 //     exceeds it by more than kSlack, so P <= 2^kSlack and the common tile needs
 //     no rescale. A score wavefront that sees such a logit uses the larger max
 //     for its own P and raises a flag; on the next tile every wavefront of the
-//     KV head reads the four maxima used, takes their maximum, and rescales its
-//     share (l, O, and the P values of that tile) onto it.
-//   * PV: v_mfma_f32_16x16x32_f16 with fp32 accumulation. P enters as an fp16
-//     hi + lo pair (~22 bits); V = (nib - 8) * d_v (the code from the exact fp16
-//     integer 1024 + nib minus 1032) as an fp16 hi + lo pair that holds it
-//     exactly, so O += Ph Vh + Pl Vh + Ph Vl: three MFMAs, every product exact
-//     in fp32. A row that a few keys dominate then carries no fp16 rounding of
-//     V or P into its output (ggml's CPU path dequantizes V to fp32 exactly).
+//     workgroup reads the four maxima used, takes their maximum, and rescales
+//     its share (l, O, and the P values of that tile) onto it.
+//   * PV: v_mfma_f32_16x16x32_f16 with fp32 accumulation, d_v on the A side:
+//     A = P d_v of the block as an exact fp16 hi + lo pair (P arrives as an fp16
+//     hi + lo pair, ~22 bits), B = the raw nibbles as fp16 subnormals (nib *
+//     2^-24, or nib * 2^-20 for the high nibble, one v_and per two keys), and
+//     the -8 offset as -8 * sum A from one more MFMA against ones. Every product
+//     is exact in fp32, so a row that a few keys dominate carries no fp16
+//     rounding of V or P into its output (ggml's CPU path dequantizes V to fp32
+//     exactly). P is kept at 2^-4 of its value (<= 16), so A stays finite for
+//     every |d_v| < 4094, i.e. V values up to 32752 in magnitude.
 //   * A key that no row of the call sees (masked in every row, past the split
 //     or past the cache end) contributes exactly 0 whatever its bytes, as in
 //     ggml's CPU loop, which skips masked keys: a -inf mask entry replaces the
@@ -68,38 +77,40 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
-constexpr int kScoreWaves = 8;
-constexpr int kValueWaves = 8;
+constexpr int kScoreWaves = 4;
+constexpr int kValueWaves = 4;
 constexpr int kWaves = kScoreWaves + kValueWaves;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTileKeys = 64;
-constexpr int kKStages = 4;
+constexpr int kKStages = 3;
 constexpr int kVStages = 3;
-constexpr int kRowBytes = 2 * kHeadRowBytes;          // 288: one cache row, both KV heads
-constexpr int kLdsRow = kRowBytes + 16;               // 304
-constexpr int kSlotsPerRow = kLdsRow / 16;            // 19 (18 data chunks + pad)
-constexpr int kTensorBytes = kTileKeys * kLdsRow;     // 19456
-constexpr int kTensorInsts = kTensorBytes / 1024;     // 19 DMA instructions of 64 x 16 B
+constexpr int kCacheRow = 2 * kHeadRowBytes;          // 288: one cache row, both KV heads
+constexpr int kSlotsPerRow = 10;                      // 9 data chunks + a pad chunk
+constexpr int kLdsRow = 16 * kSlotsPerRow;            // 160
+constexpr int kTensorBytes = kTileKeys * kLdsRow;     // 10240
+constexpr int kTensorInsts = kTensorBytes / 1024;     // 10 DMA instructions of 64 x 16 B
 constexpr int kMaxMaskRows = 4;                       // query positions
 constexpr int kMaskStageBytes = kMaxMaskRows * kTileKeys * 2;
 constexpr int kPRow = 136;                            // fp16 P row: 64 keys hi, 64 keys lo, 8 pad
-constexpr int kPHeadBytes = 16 * kPRow * 2;           // 16 query rows
 // LDS map
 constexpr int kOffV = kKStages * kTensorBytes;
 constexpr int kOffMask = kOffV + kVStages * kTensorBytes;
 constexpr int kOffDk = kOffMask + kKStages * kMaskStageBytes;  // per score wave [8 blocks][16 keys] fp16
 constexpr int kOffDv = kOffDk + kScoreWaves * 256;             // per value wave [2 blocks][2 halves][4][8] fp16
-constexpr int kOffP = kOffDv + kValueWaves * 256;              // [2 tiles][2 heads][16 rows][kPRow] fp16 hi|lo
-constexpr int kOffM = kOffP + 2 * 2 * kPHeadBytes;             // [2 tiles][2 heads][4 waves][16 rows] f32
-constexpr int kOffFlag = kOffM + 2 * 2 * 4 * 16 * 4;           // [2 tiles][2 heads][4 waves] u32
-constexpr int kOffL = kOffFlag + 2 * 2 * 4 * 4;                // [2 heads][4 waves][16 rows] f32
-constexpr int kLdsBytes = kOffL + 2 * 4 * 16 * 4;
+constexpr int kOffP = kOffDv + kValueWaves * 256;              // [2 tiles][16 rows][kPRow] fp16 hi|lo
+constexpr int kOffM = kOffP + 2 * 16 * kPRow * 2;              // [2 tiles][4 waves][16 rows] f32
+constexpr int kOffFlag = kOffM + 2 * 4 * 16 * 4;               // [2 tiles][4 waves] u32
+constexpr int kOffL = kOffFlag + 2 * 4 * 4;                    // [4 waves][16 rows] f32
+constexpr int kLdsBytes = kOffL + 4 * 16 * 4;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kSlack = 8.0f;  // log2 of the largest P the lazy rescale admits
+// P is stored as P 2^-kPShift (<= 2^(kSlack - kPShift) = 16) and l summed from the
+// same values, so A = P d_v stays below 65504 for every |d_v| < 4094.
+constexpr float kPShift = 4.0f;
 static_assert(kTensorBytes % 1024 == 0, "a tile tensor must be whole DMA instructions");
-static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
-static_assert(2 * 4 * 2 * 64 * 32 <= (kVStages - 1) * kTensorBytes, "Q operands must fit in V stages 1..2");
+static_assert(2 * kLdsBytes <= 160 * 1024, "two workgroups per CU");
+static_assert(4 * 2 * 64 * 32 <= (kVStages - 1) * kTensorBytes, "Q operands must fit in V stages 1..2");
 
 // 16 bytes per lane from sbase + voff into LDS at m0 + 16 * lane. The data
 // arrives asynchronously; the caller waits with s_waitcnt vmcnt.
@@ -124,7 +135,7 @@ __device__ __forceinline__ void wait_vm_barrier(int n) {
     case N: asm volatile("s_waitcnt vmcnt(" #N ") lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
         SQA_WAIT_CASE(0) SQA_WAIT_CASE(1) SQA_WAIT_CASE(2) SQA_WAIT_CASE(3) SQA_WAIT_CASE(4)
         SQA_WAIT_CASE(5) SQA_WAIT_CASE(6) SQA_WAIT_CASE(7) SQA_WAIT_CASE(8) SQA_WAIT_CASE(9)
-        SQA_WAIT_CASE(10) SQA_WAIT_CASE(11) SQA_WAIT_CASE(12)
+        SQA_WAIT_CASE(10) SQA_WAIT_CASE(11) SQA_WAIT_CASE(12) SQA_WAIT_CASE(13) SQA_WAIT_CASE(14)
 #undef SQA_WAIT_CASE
         default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
     }
@@ -151,42 +162,44 @@ struct DecodeParams {
     int64_t n_kv;
     float qscale;           // softmax scale * log2(e)
     int n_splits;
+    int split_tiles;        // 64-key tiles of every split; the first split_extra splits take one more
+    int split_extra;
     float *part_acc;        // [n_splits][n_q*H][256]
     float *part_ml;         // [n_splits][n_q*H][2]
 };
 
-// Per-lane byte offsets of the tile DMA: slot s = 64*j + lane of instruction j
-// holds chunk min(s % 19, 17) of row s / 19 (chunk 18 is the pad).
-__device__ __forceinline__ uint32_t tile_slot_offset(int j, int lane) {
-    const int s = 64 * j + lane;
-    const int row = s / kSlotsPerRow;
-    const int col = s - row * kSlotsPerRow;
-    return (uint32_t)(row * kRowBytes + (col < 17 ? col : 17) * 16);
-}
-
-// V tiles land rotated: row r's 16-byte chunks start 2*((r >> 3) & 3) slots later
-// (mod 19), so the four 8-row key groups that a value wavefront reads together
-// sit on disjoint banks.
+// Chunk rotation of an LDS row: K rows 8-15 of every 16-row group start one
+// slot later, V rows two slots later per 8-row group (mod kSlotsPerRow).
+__device__ __forceinline__ int k_rot(int row) { return (row >> 3) & 1; }
 __device__ __forceinline__ int v_rot(int row) { return 2 * ((row >> 3) & 3); }
-__device__ __forceinline__ uint32_t v_slot_offset(int j, int lane) {
+
+// Per-lane source offset of DMA instruction j of a tile stage: slot s = 64*j +
+// lane lands at LDS byte 16*s, i.e. slot s % 10 of row s / 10, and holds chunk
+// (slot - rot) mod 10 of that row's head half (chunk 9, the pad, repeats chunk 8).
+template <bool V>
+__device__ __forceinline__ uint32_t slot_offset(int j, int lane, int kvh) {
     const int s = 64 * j + lane;
     const int row = s / kSlotsPerRow;
     const int slot = s - row * kSlotsPerRow;
-    int c = slot - v_rot(row);
+    int c = slot - (V ? v_rot(row) : k_rot(row));
     c = c < 0 ? c + kSlotsPerRow : c;
-    return (uint32_t)(row * kRowBytes + (c < 17 ? c : 17) * 16);
+    return (uint32_t)(row * kCacheRow + kvh * kHeadRowBytes + (c < 8 ? c : 8) * 16);
 }
-// LDS byte of cache-row byte c (0..287) of V row `row` inside a tile stage
-__device__ __forceinline__ int v_lds_byte(int row, int c) {
-    int slot = (c >> 4) + v_rot(row);
+// LDS byte of head-row byte c (0..143) of row `row` inside a tile stage
+template <bool V>
+__device__ __forceinline__ int lds_byte(int row, int c) {
+    int slot = (c >> 4) + (V ? v_rot(row) : k_rot(row));
     slot = slot >= kSlotsPerRow ? slot - kSlotsPerRow : slot;
     return row * kLdsRow + slot * 16 + (c & 15);
 }
 
 // TWO = false: up to 8 query rows per KV head (one block-diagonal B set).
 // TWO = true : 9..16 rows (rows 0-7 and 8-15 as two B sets, one A operand).
+// Both forms must stay within 128 VGPRs so that two workgroups share a CU: the
+// 8-row form is held there by its bound (4 waves per SIMD); the 16-row form
+// allocates 127 by itself and spills if it is bound the same way.
 template <bool TWO>
-__global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(DecodeParams p) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
@@ -194,15 +207,20 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
     const int g = lane >> 4;
     const int n = lane & 15;
     const bool score = wave < kScoreWaves;
-    const int kvh = (wave >> 2) & 1;  // KV head of this wavefront
-    const int wq = wave & 3;          // score: 16-key quarter of every tile; value: 64-dim slice
+    const int wq = wave & 3;  // score: 16-key quarter of every tile; value: 64-dim slice
     const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
     constexpr int kRowMask = TWO ? 15 : 7;  // rows 8-15 mirror rows 0-7 when only 8 exist
 
-    // ---------------- key range of this split --------------------------------
-    const int split = blockIdx.x;
-    int64_t k0 = (p.n_kv * split / p.n_splits) & ~(int64_t)7;
-    int64_t k1 = split + 1 == p.n_splits ? p.n_kv : ((p.n_kv * (split + 1) / p.n_splits) & ~(int64_t)7);
+    // ---------------- split and KV head of this workgroup ---------------------
+    // Workgroups go round-robin to the 8 XCDs: ids 16a + 8h + x (x < 8) are split
+    // 8a + x, head h, so both heads of a split share an XCD (and its L2).
+    const int id = blockIdx.x;
+    const int kvh = (id >> 3) & 1;
+    const int split = ((id >> 4) << 3) | (id & 7);
+    const int t_begin = split * p.split_tiles + (split < p.split_extra ? split : p.split_extra);
+    const int64_t k0 = (int64_t)t_begin * kTileKeys;
+    int64_t k1 = k0 + (int64_t)(p.split_tiles + (split < p.split_extra ? 1 : 0)) * kTileKeys;
+    if (k1 > p.n_kv) k1 = p.n_kv;
     if (p.q_pos0 >= 0 && k1 > p.q_pos0 + p.n_q) k1 = p.q_pos0 + p.n_q;  // no row sees past this
     const int n_tiles = k1 > k0 ? (int)((k1 - k0 + kTileKeys - 1) / kTileKeys) : 0;
 
@@ -219,9 +237,9 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
         // Q -> q8_0 block-diagonal B operands. Column n of C: row r = (n & 7)
         // [+ 8 for the second set], block 2*pair + (n >> 3). Lane (g, n) supplies
         // k = 16g..16g+15, i.e. values 16*(g&1).. of the column's block when
-        // (g >> 1) == (n >> 3), zeros otherwise. The four wavefronts of a KV head
-        // each load their block pair (pair = wq) of the Q rows straight from global
-        // memory at entry, quantise it and exchange the operands through LDS.
+        // (g >> 1) == (n >> 3), zeros otherwise. The four wavefronts each load
+        // their block pair (pair = wq) of the Q rows straight from global memory
+        // at entry, quantise it and exchange the operands through LDS.
         constexpr int kSets = TWO ? 2 : 1;
         constexpr int kOpndBytes = 32;  // per lane: 16 code bytes, d_q, -8*sum(q8)
         int32x4 bq[kSets][4];
@@ -284,7 +302,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             }
 #pragma unroll
             for (int set = 0; set < kSets; ++set) {
-                uint8_t *o = qs_lds + (((kvh * 4 + pr) * kSets + set) * 64 + lane) * kOpndBytes;
+                uint8_t *o = qs_lds + ((pr * kSets + set) * 64 + lane) * kOpndBytes;
                 *reinterpret_cast<int32x4 *>(o) = my_bq[set];
                 *reinterpret_cast<float2 *>(o + 16) = make_float2(my_dq[set], __int_as_float(my_ci[set]));
             }
@@ -293,7 +311,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             for (int pp = 0; pp < 4; ++pp)
 #pragma unroll
                 for (int set = 0; set < kSets; ++set) {
-                    const uint8_t *o = qs_lds + (((kvh * 4 + pp) * kSets + set) * 64 + lane) * kOpndBytes;
+                    const uint8_t *o = qs_lds + ((pp * kSets + set) * 64 + lane) * kOpndBytes;
                     bq[set][pp] = *reinterpret_cast<const int32x4 *>(o);
                     const float2 dc = *reinterpret_cast<const float2 *>(o + 16);
                     dqs[set][pp] = dc.x;
@@ -306,15 +324,25 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
         const int my_t = my_ok ? my_r / p.G : 0;
         const bool row_writer = TWO || n < 8;  // lanes n >= 8 mirror rows 0-7 when only 8 exist
         // K operand: lane (g, n) reads key n's block 2*pair + (g >> 1), nibbles of half g & 1.
-        // qs of block b sits at 18b + 2 in the head row: 4-aligned for odd b, 2 mod 4 for even b.
+        // qs of block b sits at 18b + 2 in the head row: 4-aligned for odd b, 2 mod 4 for
+        // even b. The five dwords from the aligned address below it stay inside two
+        // adjacent slots of the row (block 7 spills one unused dword into the next).
         const int ka_blk_par = g >> 1;
         const uint32_t ka_shift = (ka_blk_par ? 0u : 16u) + 4u * (uint32_t)(g & 1);
         uint8_t *dk_comp = smem + kOffDk + wave * 256;  // [8 blocks][16 keys] fp16
         const int key0 = 16 * wq;                       // first key of this wavefront in a tile
         // P is stored in key order: this lane's four keys key0 + 4g + i
         const int p_col = key0 + 4 * g;
+        int ka_off[4];  // LDS offsets of this lane's K windows (block pair pr), within a stage
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr)
+            ka_off[pr] = lds_byte<false>(key0 + n, (18 * (2 * pr + ka_blk_par) + 2) & ~3);
+        // d_k compaction: lane -> block lane >> 3, keys key0 + 4gg + 2hh and the next one
+        const int dk_blk = lane >> 3, dk_gg = lane & 3, dk_hh = (lane >> 2) & 1;
+        const int dk_src = lds_byte<false>(key0 + 4 * dk_gg + 2 * dk_hh, 18 * dk_blk);
+        const int dk_dst = (dk_blk * 16 + 4 * dk_gg + 2 * dk_hh) * 2;
 
-        float m_ref = -INFINITY;   // base-2 reference max of row my_r (common to the KV head)
+        float m_ref = -INFINITY;   // base-2 reference max of row my_r (common to the workgroup)
         float m_used = -INFINITY;  // reference this wavefront used for the last tile's P
         float l_acc = 0.0f;        // this lane's share of the row's sum, relative to m_ref
         float l_prev = 0.0f;       // the last tile's share, relative to m_used
@@ -324,12 +352,12 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             const int t = TWO ? __builtin_amdgcn_readfirstlane(tt) : tt;
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // K(t) and P(t-1) readable
 
-            // -- fold the last tile's sum into l under the KV head's common max --
+            // -- fold the last tile's sum into l under the workgroup's common max --
             if (t > 0) {
                 const int pb = (t - 1) & 1;
-                const uint4 fl = *reinterpret_cast<const uint4 *>(fbuf + (pb * 2 + kvh) * 4);
+                const uint4 fl = *reinterpret_cast<const uint4 *>(fbuf + pb * 4);
                 if ((fl.x | fl.y | fl.z | fl.w) & 1u) {
-                    const float *mr = mbuf + (pb * 2 + kvh) * 64;
+                    const float *mr = mbuf + pb * 64;
                     const float mn = fmaxf(fmaxf(mr[my_r], mr[16 + my_r]), fmaxf(mr[32 + my_r], mr[48 + my_r]));
                     l_acc = l_acc * exp2_or_zero(m_ref, mn) + l_prev * exp2_or_zero(m_used, mn);
                     m_ref = mn;
@@ -340,19 +368,15 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             if (t == n_tiles) break;
 
             const int64_t kt = k0 + (int64_t)t * kTileKeys;
-            const int st = t & (kKStages - 1);
-            const uint8_t *sK = smem + st * kTensorBytes + kvh * kHeadRowBytes;
+            const int st = t % kKStages;
+            const uint8_t *sK = smem + st * kTensorBytes;
             // a tile holding keys past the range end or past a causal limit
             const bool tail = kt + kTileKeys > k1 || (p.q_pos0 >= 0 && kt + kTileKeys - 1 > p.q_pos0);
 
             // A row r of QK is key key0 + r, so lane group g holds keys key0 + 4g + i.
             // -- compact d_k of those keys, [block][4g + i] ------------------------
-            {
-                const int blk = lane >> 3, gg = lane & 3, hh = (lane >> 2) & 1;
-                const uint8_t *src = sK + (key0 + 4 * gg + 2 * hh) * kLdsRow + 18 * blk;
-                *reinterpret_cast<uint32_t *>(dk_comp + (blk * 16 + 4 * gg + 2 * hh) * 2) =
-                    lds16(src) | (lds16(src + kLdsRow) << 16);
-            }
+            *reinterpret_cast<uint32_t *>(dk_comp + dk_dst) =
+                lds16(sK + dk_src) | (lds16(sK + dk_src + kLdsRow) << 16);
 
             // -- QK: xs[i] = S[key key0+4g+i][row of column n] --------------------
             float xs[kSets][4];
@@ -360,12 +384,11 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             for (int set = 0; set < kSets; ++set)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) xs[set][i] = 0.0f;
-            const uint8_t *krow = sK + (key0 + n) * kLdsRow;
 #pragma unroll
             for (int pr = 0; pr < 4; ++pr) {
                 // key of A row n, block 2*pair + (g >> 1): five dwords from the aligned
                 // address below its 16 qs bytes, shifted to the nibble half g & 1
-                const uint8_t *ap = krow + ((18 * (2 * pr + ka_blk_par) + 2) & ~3);
+                const uint8_t *ap = sK + ka_off[pr];
                 const uint32_t w0 = lds32(ap), w1 = lds32(ap + 4), w2 = lds32(ap + 8), w3 = lds32(ap + 12),
                                w4 = lds32(ap + 16);
                 uint32_t aw[4];
@@ -438,7 +461,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             const float mb = mu == -INFINITY ? 0.0f : mu;
             float pv[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_exp2f(s[i] - mb);
+            for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_exp2f(s[i] - mb - kPShift);
             l_prev = (pv[0] + pv[1]) + (pv[2] + pv[3]);
             const int buf = t & 1;
             if (row_writer) {
@@ -455,10 +478,10 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                         asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[0,0,0] op_sel_hi:[0,0,1]" : "=v"(r[i]) : "v"(pv[i]), "v"(hw[i >> 1]));
                 }
                 pl = half4{(_Float16)r[0], (_Float16)r[1], (_Float16)r[2], (_Float16)r[3]};
-                _Float16 *prow = pbuf + ((buf * 2 + kvh) * 16 + my_r) * kPRow + p_col;
+                _Float16 *prow = pbuf + (buf * 16 + my_r) * kPRow + p_col;
                 *reinterpret_cast<half4 *>(prow) = ph;
                 *reinterpret_cast<half4 *>(prow + 64) = pl;
-                if (g == 0) mbuf[((buf * 2 + kvh) * 4 + wq) * 16 + my_r] = mu;
+                if (g == 0) mbuf[(buf * 4 + wq) * 16 + my_r] = mu;
             }
             // keys of this wavefront that some row sees: bit 4g + i of the 16
             uint32_t alive16 = 0;
@@ -468,17 +491,16 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
 #pragma unroll
                 for (int gg = 0; gg < 4; ++gg) alive16 |= ((b >> (16 * gg)) & 0xFFFFu) ? 1u << (4 * gg + i) : 0u;
             }
-            if (lane == 0) fbuf[(buf * 2 + kvh) * 4 + wq] = (need ? 1u : 0u) | (alive16 << 16);
+            if (lane == 0) fbuf[buf * 4 + wq] = (need ? 1u : 0u) | (alive16 << 16);
         }
 
         // ---------------- this split's softmax statistics ------------------------
         l_acc += __shfl_xor(l_acc, 16);
         l_acc += __shfl_xor(l_acc, 32);
-        if (g == 0 && row_writer) lbuf[(kvh * 4 + wq) * 16 + my_r] = l_acc;
+        if (g == 0 && row_writer) lbuf[wq * 16 + my_r] = l_acc;
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (wq == 0 && g == 0 && row_writer && my_ok) {
-            const float *lr = lbuf + kvh * 64;
-            const float L = (lr[my_r] + lr[16 + my_r]) + (lr[32 + my_r] + lr[48 + my_r]);
+            const float L = (lbuf[my_r] + lbuf[16 + my_r]) + (lbuf[32 + my_r] + lbuf[48 + my_r]);
             const int tq = my_r / p.G, hq = kvh * p.G + my_r % p.G;
             const int64_t ridx = (int64_t)split * rows_total + (int64_t)tq * p.H + hq;
             p.part_ml[ridx * 2 + 0] = m_ref == -INFINITY ? m_ref : m_ref * kLn2;  // combine works in base e
@@ -488,17 +510,17 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
         // ============ value wavefronts: O[rows][64 dims] += P V =================
         // ---------------- DMA plan of this wavefront ---------------------------
         // Value wavefronts issue every DMA (score wavefronts carry no DMA state):
-        // 19 K + 19 V instructions per tile, K j -> value wave j % 8, V j -> value
-        // wave (j + 3) % 8, the mask rows -> value wave 7 (4 or 5 per wavefront).
+        // 10 K + 10 V instructions per tile, K j -> value wave j % 4, V j -> value
+        // wave (j + 2) % 4, the mask rows -> value wave 3 (5 or 6 per wavefront).
         const int vw = wave - kScoreWaves;
         uint32_t koff[3], voff[3];
         int nk = 0, nv = 0;
 #pragma unroll
         for (int r = 0; r < 3; ++r) {
-            const int jk = vw + 8 * r;
-            const int jv = ((vw + 5) & 7) + 8 * r;
-            koff[r] = tile_slot_offset(jk < kTensorInsts ? jk : 0, lane);
-            voff[r] = v_slot_offset(jv < kTensorInsts ? jv : 0, lane);
+            const int jk = vw + 4 * r;
+            const int jv = ((vw + 2) & 3) + 4 * r;
+            koff[r] = slot_offset<false>(jk < kTensorInsts ? jk : 0, lane, kvh);
+            voff[r] = slot_offset<true>(jv < kTensorInsts ? jv : 0, lane, kvh);
             nk += jk < kTensorInsts;
             nv += jv < kTensorInsts;
         }
@@ -510,118 +532,97 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
 
         // keys past the cache end re-read its last row (they are masked off)
         auto lim_of = [&](int64_t kt) -> uint32_t {
-            return p.n_kv - kt >= kTileKeys ? 0xFFFFFFFFu : (uint32_t)((p.n_kv - kt) * kRowBytes - 16);
+            return p.n_kv - kt >= kTileKeys ? 0xFFFFFFFFu : (uint32_t)((p.n_kv - kt) * kCacheRow - 16);
         };
         auto issue_k = [&](int t) {
             const int64_t kt = k0 + (int64_t)t * kTileKeys;
             const uint32_t lim = lim_of(kt);
-            const uint8_t *kb = p.k + kt * kRowBytes;
-            const uint32_t kbase = lds0 + (t & (kKStages - 1)) * kTensorBytes;
+            const uint8_t *kb = p.k + kt * kCacheRow;
+            const int st = t % kKStages;
+            const uint32_t kbase = lds0 + st * kTensorBytes;
 #pragma unroll
             for (int r = 0; r < 3; ++r)
-                if (r < nk) dma16(koff[r] < lim ? koff[r] : lim, kb, kbase + 1024u * (vw + 8 * r));
+                if (r < nk) dma16(koff[r] < lim ? koff[r] : lim, kb, kbase + 1024u * (vw + 4 * r));
             if (mask_dma) {
                 const uint32_t mlim =
                     p.mask_len - kt >= kTileKeys + 8 ? 0xFFFFFFFFu : (uint32_t)((p.mask_len - 8 - kt) * 2);
                 const uint32_t mo = moff - 16 * (lane & 7) + ((16u * (lane & 7)) < mlim ? 16u * (lane & 7) : mlim);
-                if (mrow_l < p.n_q)
-                    dma16(mo, p.mask + kt * 2, lds0 + kOffMask + (t & (kKStages - 1)) * kMaskStageBytes);
+                if (mrow_l < p.n_q) dma16(mo, p.mask + kt * 2, lds0 + kOffMask + st * kMaskStageBytes);
             }
         };
-        auto issue_v = [&](int t, int stage) {
+        auto issue_v = [&](int t) {
             const int64_t kt = k0 + (int64_t)t * kTileKeys;
             const uint32_t lim = lim_of(kt);
-            const uint8_t *vb = p.v + kt * kRowBytes;
-            const uint32_t vbase = lds0 + kOffV + stage * kTensorBytes;
+            const uint8_t *vb = p.v + kt * kCacheRow;
+            const uint32_t vbase = lds0 + kOffV + (t % kVStages) * kTensorBytes;
 #pragma unroll
             for (int r = 0; r < 3; ++r)
-                if (r < nv) dma16(voff[r] < lim ? voff[r] : lim, vb, vbase + 1024u * (((vw + 5) & 7) + 8 * r));
+                if (r < nv) dma16(voff[r] < lim ? voff[r] : lim, vb, vbase + 1024u * (((vw + 2) & 3) + 4 * r));
         };
         // DMA instructions this wavefront issued after the last one that interval t
-        // needs (K of tile t, V of tile t-1): the loop issues K(t+3) and V(t+1) at
-        // interval t, after K 0-2 and V 0 before the loop.
+        // needs (K of tile t, V of tile t-1): the loop issues K(t+2) and V(t+1) at
+        // interval t, after K 0, K 1 and V 0 before the loop, so at interval t's
+        // barrier the younger ones are K(t+1) and V(t) (interval t-1's pair, or K 1
+        // and V 0 for t = 0).
         auto younger_than_needed = [&](int t) -> int {
-            if (t == 0) return (n_tiles > 1 ? per_k : 0) + (n_tiles > 2 ? per_k : 0) + (n_tiles > 0 ? per_v : 0);
-            return (t + 2 < n_tiles ? per_k : 0) + (t < n_tiles ? per_v : 0);
+            return (t + 1 < n_tiles ? per_k : 0) + (t < n_tiles ? per_v : 0);
         };
 
-        // ---------------- K 0-2 and V 0 ------------------------------------------
-        const int pre = n_tiles < kKStages - 1 ? n_tiles : kKStages - 1;
-        for (int t = 0; t < pre; ++t) issue_k(t);
-        if (n_tiles > 0) issue_v(0, 0);
+        // ---------------- K 0-1 and V 0 ------------------------------------------
+        // (V stages 1-2 hold the Q operands until the loop's first barrier)
+        if (n_tiles > 0) issue_k(0);
+        if (n_tiles > 1) issue_k(1);
+        if (n_tiles > 0) issue_v(0);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // Q operands published
         const int dq = wq;  // dims 64dq..64dq+63: blocks 2dq, 2dq+1
-        // Nibble -> exact fp16 integer: the low nibble in mantissa bits 0-3 under
-        // exponent 10 is 1024 + lo; the high nibble left in bits 4-7 under exponent
-        // 6 is 64 + hi. Both constants sit in VGPRs so v_and_or_b32 takes them.
-        uint32_t magic_lo, magic_hi;
-        asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic_lo));
-        asm volatile("v_mov_b32 %0, 0x54005400" : "=v"(magic_hi));
-        const half2v off_lo = {(_Float16)-1032.0f, (_Float16)-1032.0f};  // 1024 + 8
-        const half2v off_hi = {(_Float16)-72.0f, (_Float16)-72.0f};      // 64 + 8
-        uint8_t *dv_comp = smem + kOffDv + (wave - kScoreWaves) * 256;  // [bl][half][g][j] fp16
+        // B operand straight from the nibbles: a nibble in the low bits of an fp16
+        // is the subnormal nib * 2^-24 (low nibble) or, left in bits 4-7,
+        // nib * 2^-20 (high nibble), exact values that the MFMA multiplies exactly.
+        const half8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+        uint8_t *dv_comp = smem + kOffDv + vw * 256;  // [bl][half][g][j] fp16
         const int ra = n & kRowMask;  // P row of this lane's A operand
         // d_v compaction: lane -> block bl, half h, key group gg, pair jj: keys
         // 32h + 8gg + 2jj and the next one (B k-slots 8gg + 2jj, +1)
         const int cbl = lane >> 5, ch = (lane >> 4) & 1, cgg = (lane >> 2) & 3, cjj = lane & 3;
         const int ckey = 32 * ch + 8 * cgg + 2 * cjj;
         const int cdst = ((cbl * 2 + ch) * 4 + cgg) * 16 + 4 * cjj;  // bytes
-        const uint32_t csrc = (uint32_t)v_lds_byte(ckey, kvh * kHeadRowBytes + 18 * (2 * dq + cbl));
+        const uint32_t csrc = (uint32_t)lds_byte<true>(ckey, 18 * (2 * dq + cbl));
         // V bytes of this lane: B k-slot 8g + j is key 32h + 8g + j; its byte n of block
-        // 2dq + bl sits at column c = kvh*144 + 2 + 18*(2dq + bl) + n of the row, rotated
-        // by v_rot = 2g chunks for every row the lane reads; the dword holding it carries
+        // 2dq + bl sits at byte c = 2 + 18*(2dq + bl) + n of the head row, rotated by
+        // v_rot = 2g slots for every row the lane reads; the dword holding it carries
         // it as byte c & 3.
         uint32_t vlane[2], vsel[2];  // v_perm selector: byte c&3 of the lower key's dword -> bits 0-7, of the upper -> 16-23
 #pragma unroll
         for (int bl = 0; bl < 2; ++bl) {
-            const int c = kvh * kHeadRowBytes + 2 + 18 * (2 * dq + bl) + n;
-            vlane[bl] = (uint32_t)(v_lds_byte(8 * g, c) & ~3);
+            const int c = 2 + 18 * (2 * dq + bl) + n;
+            vlane[bl] = (uint32_t)(lds_byte<true>(8 * g, c) & ~3);
             const uint32_t b = (uint32_t)(c & 3);
             vsel[bl] = b | (0x0cu << 8) | ((4u + b) << 16) | (0x0cu << 24);
         }
 
-        floatx4 acc[4];  // O[row 4g+i][dim 64dq + 16T + n]; T = 2*bl + (high nibble)
+        // acc[2bl] = 2^-24 sum_k A nib_lo, acc[2bl + 1] = 2^-20 sum_k A nib_hi, and
+        // cor[bl] = sum_k A, with A = P d_v of block 2dq + bl, so that
+        // O[row 4g+i][dim 64dq + 32bl + n (+16 for the high nibble)] = 2^24 acc - 8 cor.
+        floatx4 acc[4], cor[2];
 #pragma unroll
         for (int T = 0; T < 4; ++T) acc[T] = floatx4{0.f, 0.f, 0.f, 0.f};
+        cor[0] = cor[1] = floatx4{0.f, 0.f, 0.f, 0.f};
         float m_acc[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // reference max of rows 4g+i
 
         for (int tt = 0; tt <= n_tiles; ++tt) {
             const int t = TWO ? __builtin_amdgcn_readfirstlane(tt) : tt;  // wave-uniform tile index
             wait_vm_barrier(younger_than_needed(t));
-            if (t + kKStages - 1 < n_tiles) issue_k(t + kKStages - 1);
-            if (t + 1 < n_tiles) issue_v(t + 1, (t + 1) % kVStages);
+            if (t + 2 < n_tiles) issue_k(t + 2);
+            if (t + 1 < n_tiles) issue_v(t + 1);
             if (t == 0) continue;
 
             const int tv = t - 1;  // PV of the tile whose P the score wavefronts wrote last
             const int pb = tv & 1;
-            const int64_t kt = k0 + (int64_t)tv * kTileKeys;
             const uint32_t sv_off = (uint32_t)(kOffV + (tv % kVStages) * kTensorBytes);  // wave-uniform
-
-            // -- the slice's V bytes for all 64 keys: 16 registers, two keys each ---
-            // x[4*(2h + bl) + m] holds keys 32h + 8g + 2m (bits 0-7) and 32h + 8g + 2m + 1
-            // (bits 16-23), byte n of block 2dq + bl's qs: adjacent rows, one ds_read2_b32
-            // each. A base per two pairs keeps both dword offsets within ds_read2's 8 bits.
-            uint32_t x[16];
-#pragma unroll
-            for (int bl = 0; bl < 2; ++bl)
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-#pragma unroll
-                    for (int mp = 0; mp < 2; ++mp) {
-                        uint32_t va = lds0 + sv_off + vlane[bl] + (uint32_t)((32 * h + 4 * mp) * kLdsRow);
-                        asm volatile("" : "+v"(va));  // opaque: no induction variable per address
-                        const lds_u32 *r0 = reinterpret_cast<const lds_u32 *>((uintptr_t)va);
-#pragma unroll
-                        for (int m2 = 0; m2 < 2; ++m2) {
-                            const int m = 2 * mp + m2;
-                            x[4 * (2 * h + bl) + m] = __builtin_amdgcn_perm(r0[(2 * m2 + 1) * (kLdsRow / 4)],
-                                                                            r0[2 * m2 * (kLdsRow / 4)], vsel[bl]);
-                        }
-                    }
 
             // flags of the score wavefronts: bit 0 = maximum moved, bits 16-31 = their
             // 16 keys that some row of the call can see (P != 0)
-            const uint4 fl = *reinterpret_cast<const uint4 *>(fbuf + (pb * 2 + kvh) * 4);
+            const uint4 fl = *reinterpret_cast<const uint4 *>(fbuf + pb * 4);
 
             // -- d_v of the slice's two blocks for all 64 keys, in B k-slot order --
             // A key no row sees (masked, past the range or past the cache end) gets
@@ -638,14 +639,14 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             }
 
             // -- P rows (k-slot order) and a possible move of the reference max ---
-            const _Float16 *prow = pbuf + ((pb * 2 + kvh) * 16 + ra) * kPRow + 8 * g;
+            const _Float16 *prow = pbuf + (pb * 16 + ra) * kPRow + 8 * g;
             half8 pa[2], pl[2];  // P hi and lo of tile halves 0, 1
             pa[0] = *reinterpret_cast<const half8 *>(prow);
             pa[1] = *reinterpret_cast<const half8 *>(prow + 32);
             pl[0] = *reinterpret_cast<const half8 *>(prow + 64);
             pl[1] = *reinterpret_cast<const half8 *>(prow + 96);
             if ((fl.x | fl.y | fl.z | fl.w) & 1u) {
-                const float *mr = mbuf + (pb * 2 + kvh) * 64;
+                const float *mr = mbuf + pb * 64;
                 float fac[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -657,6 +658,8 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                 const floatx4 f4 = {fac[0], fac[1], fac[2], fac[3]};
 #pragma unroll
                 for (int T = 0; T < 4; ++T) acc[T] *= f4;
+                cor[0] *= f4;
+                cor[1] *= f4;
                 // P of score wavefront w (keys 16w..16w+15: this lane's half-h slots 8g..8g+7
                 // come from wavefront 2h + (g >> 1)) onto the new max
                 float mw[4];
@@ -674,46 +677,53 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
             }
 
             // -- O += P V over the two halves of the tile and the slice's blocks ---
-            // V = (nib - 8) * d_v exactly, as Vh + Vl: Vh = fp16(V) and Vl = V - Vh by
-            // one fma. A code has at most 3 significant bits and d_v 11, so V has at
-            // most 14 and the residual at most 3: both halves are exact in fp16. With
-            // P as hi + lo, O += Ph Vh + Pl Vh + Ph Vl (Pl Vl is below 2^-22 of PV).
+            // A = P d_v exactly as Ah + Al in packed fp16: Ph d_v has at most 22
+            // significant bits, so its residual after rounding to fp16 (at most 11) is
+            // exact in one fma; Pl d_v is 2^-11 of it and rounds once. Every MFMA
+            // product is then exact in fp32, and V's -8 offset comes in as -8 sum A.
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
+                // the slice's V bytes for the 32 keys of this half, two keys per register:
+                // x[4*bl + m] holds keys 32h + 8g + 2m (bits 0-7) and 32h + 8g + 2m + 1
+                // (bits 16-23), byte n of block 2dq + bl's qs: adjacent rows, one
+                // ds_read2_b32 each. A base per two pairs keeps both dword offsets within
+                // ds_read2's 8 bits.
+                uint32_t x[8];
+#pragma unroll
+                for (int bl = 0; bl < 2; ++bl)
+#pragma unroll
+                    for (int mp = 0; mp < 2; ++mp) {
+                        uint32_t va = lds0 + sv_off + vlane[bl] + (uint32_t)((32 * h + 4 * mp) * kLdsRow);
+                        asm volatile("" : "+v"(va));  // opaque: no induction variable per address
+                        const lds_u32 *r0 = reinterpret_cast<const lds_u32 *>((uintptr_t)va);
+#pragma unroll
+                        for (int m2 = 0; m2 < 2; ++m2)
+                            x[4 * bl + 2 * mp + m2] = __builtin_amdgcn_perm(r0[(2 * m2 + 1) * (kLdsRow / 4)],
+                                                                             r0[2 * m2 * (kLdsRow / 4)], vsel[bl]);
+                    }
 #pragma unroll
                 for (int bl = 0; bl < 2; ++bl) {
                     const uint4 dv4 = *reinterpret_cast<const uint4 *>(dv_comp + ((bl * 2 + h) * 4 + g) * 16);
-                    const uint32_t dvw[4] = {dv4.x, dv4.y, dv4.z, dv4.w};
-                    half8 blo, bhi, blo_r, bhi_r;
+                    half8 dv8;
+                    __builtin_memcpy(&dv8, &dv4, 16);
+                    const half8 ah = pa[h] * dv8;
+                    const half8 ar = __builtin_elementwise_fma(pa[h], dv8, -ah);
+                    const half8 al = __builtin_elementwise_fma(pl[h], dv8, ar);
+                    uint32_t wlo[4], whi[4];
 #pragma unroll
                     for (int m = 0; m < 4; ++m) {
-                        const uint32_t xm = x[4 * (2 * h + bl) + m];
-                        const uint32_t lw = (xm & 0x000F000Fu) | magic_lo;
-                        const uint32_t hw = (xm & 0x00F000F0u) | magic_hi;
-                        half2v lo, hi, dv2;
-                        __builtin_memcpy(&lo, &lw, 4);
-                        __builtin_memcpy(&hi, &hw, 4);
-                        __builtin_memcpy(&dv2, &dvw[m], 4);
-                        lo = lo + off_lo;  // nib - 8, exact
-                        hi = hi + off_hi;
-                        const half2v lo_h = lo * dv2, hi_h = hi * dv2;
-                        const half2v lo_r = __builtin_elementwise_fma(lo, dv2, -lo_h);
-                        const half2v hi_r = __builtin_elementwise_fma(hi, dv2, -hi_h);
-                        blo[2 * m] = lo_h[0];
-                        blo[2 * m + 1] = lo_h[1];
-                        bhi[2 * m] = hi_h[0];
-                        bhi[2 * m + 1] = hi_h[1];
-                        blo_r[2 * m] = lo_r[0];
-                        blo_r[2 * m + 1] = lo_r[1];
-                        bhi_r[2 * m] = hi_r[0];
-                        bhi_r[2 * m + 1] = hi_r[1];
+                        wlo[m] = x[4 * bl + m] & 0x000F000Fu;
+                        whi[m] = x[4 * bl + m] & 0x00F000F0u;
                     }
-                    acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[h], blo, acc[2 * bl], 0, 0, 0);
-                    acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[h], bhi, acc[2 * bl + 1], 0, 0, 0);
-                    acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[h], blo, acc[2 * bl], 0, 0, 0);
-                    acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[h], bhi, acc[2 * bl + 1], 0, 0, 0);
-                    acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[h], blo_r, acc[2 * bl], 0, 0, 0);
-                    acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[h], bhi_r, acc[2 * bl + 1], 0, 0, 0);
+                    half8 blo, bhi;
+                    __builtin_memcpy(&blo, wlo, 16);
+                    __builtin_memcpy(&bhi, whi, 16);
+                    acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, blo, acc[2 * bl], 0, 0, 0);
+                    acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bhi, acc[2 * bl + 1], 0, 0, 0);
+                    cor[bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ones, cor[bl], 0, 0, 0);
+                    acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, blo, acc[2 * bl], 0, 0, 0);
+                    acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bhi, acc[2 * bl + 1], 0, 0, 0);
+                    cor[bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, ones, cor[bl], 0, 0, 0);
                 }
             }
         }
@@ -727,7 +737,10 @@ __global__ __launch_bounds__(kThreads, 1) void fa_decode_kernel(DecodeParams p) 
                 const int tq = row / p.G, hq = kvh * p.G + row % p.G;
                 float *dst = p.part_acc + ((int64_t)split * rows_total + (int64_t)tq * p.H + hq) * 256 + 64 * dq + n;
 #pragma unroll
-                for (int T = 0; T < 4; ++T) dst[16 * T] = acc[T][i];
+                for (int bl = 0; bl < 2; ++bl) {
+                    dst[32 * bl] = fmaf(acc[2 * bl][i], 16777216.0f, -8.0f * cor[bl][i]);
+                    dst[32 * bl + 16] = fmaf(acc[2 * bl + 1][i], 1048576.0f, -8.0f * cor[bl][i]);
+                }
             }
         }
     }
@@ -744,12 +757,16 @@ __global__ __launch_bounds__(256) void mask_pack_kernel(const char *__restrict__
     }
 }
 
+// One split per CU, a multiple of 8 so that the workgroup numbering above holds
+// (at most kMaxSplits); at least ~4 tiles per split.
 int decode_splits(int64_t n_kv) {
-    int64_t s = (n_kv + 255) / 256;  // at least ~4 tiles per split
-    int64_t cap = device_cu_count();
+    const int64_t tiles = (n_kv + kTileKeys - 1) / kTileKeys;
+    int64_t cap = device_cu_count() / 8 * 8;
     if (cap > kMaxSplits) cap = kMaxSplits;
+    if (cap < 8) cap = 8;
+    int64_t s = (tiles + 3) / 4;
+    s = (s + 7) / 8 * 8;
     if (s > cap) s = cap;
-    if (s < 1) s = 1;
     return (int)s;
 }
 
@@ -784,6 +801,10 @@ int launch_fa_decode(const FaArgs &a, hipStream_t s) {
     p.n_kv = n_kv;
     p.qscale = a.scale * kLog2e;
     p.n_splits = decode_splits(n_kv);
+    // whole 64-key tiles per split: no tile is read by two splits
+    const int64_t tiles = (n_kv + kTileKeys - 1) / kTileKeys;
+    p.split_tiles = (int)(tiles / p.n_splits);
+    p.split_extra = (int)(tiles % p.n_splits);
     const size_t need = fa_decode_workspace(n_q, H, n_kv);
     if (!a.ws || a.ws_bytes < need)
         return set_error(SQA_ERR_WORKSPACE, "flash_attn_ext: workspace %zu bytes < %zu needed", a.ws_bytes, need);
@@ -823,11 +844,12 @@ int launch_fa_decode(const FaArgs &a, hipStream_t s) {
                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     });
     if (lds_err != hipSuccess) return hip_status(lds_err, "fa_decode LDS attribute");
+    const unsigned grid = (unsigned)(2 * p.n_splits);  // (split, KV head) pairs
     const int prof = profile_start("fa_decode", s);
     if (p.rows <= 8)
-        fa_decode_kernel<false><<<dim3((unsigned)p.n_splits), dim3(kThreads), kLdsBytes, s>>>(p);
+        fa_decode_kernel<false><<<dim3(grid), dim3(kThreads), kLdsBytes, s>>>(p);
     else
-        fa_decode_kernel<true><<<dim3((unsigned)p.n_splits), dim3(kThreads), kLdsBytes, s>>>(p);
+        fa_decode_kernel<true><<<dim3(grid), dim3(kThreads), kLdsBytes, s>>>(p);
     profile_stop(prof, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_status(e, "fa_decode launch");

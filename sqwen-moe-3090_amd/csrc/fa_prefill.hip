@@ -24,18 +24,20 @@
 //     S^T = sum over q4_0 blocks b of d_q[b] * (Kh_b.q_b + Kl_b.q_b), the
 //     products on v_mfma_f32_16x16x32_f16 (all exact in fp32) and the d_q
 //     scaling (with scale * log2 e) as an fp32 FMA; then the mask and the
-//     online softmax in fp32 (base 2, rescaled whenever a row maximum grows, so
-//     the largest P is exactly 1). P (fp32) and the rescale factors go to LDS.
+//     online softmax in fp32 (base 2, with a lazy reference maximum that moves
+//     only when a logit passes it by more than 2^8, so P <= 2^8 and most tiles
+//     need no rescale of O). P (as an fp16 hi + lo pair) and the rescale
+//     factors go to LDS.
 //   value wave 4 + w, the same 32 rows, holds their O (128 registers) one tile
-//     behind: O = alpha O + P V per block b with A = P 2^e d_v as an fp16
-//     hi + lo pair (two MFMAs, ~22 bits) and B = the exact V codes, so every
-//     product is exact in fp32. 2^e is one power of two per KV head that
-//     brings max |d_v| into [1, 2): it keeps A clear of fp16 subnormals and
-//     overflow, and cancels in O = PV / l because l is summed from the same
-//     scaled P.
-//   A masked key contributes exactly 0 even over bytes that are not valid q4_0
-//   (as ggml's CPU loop, which skips it): a -inf mask entry replaces the logit,
-//   P d_v is formed with 0 * x = 0, and NaN/Inf scales stay out of max |d_v|.
+//     behind: O = alpha O + P V per block b (alpha only when a maximum moved)
+//     with A = P d_v 2^e as an fp16 hi + lo pair built by packed fp16 ops (two
+//     MFMAs, ~22 bits) and B = the exact V codes, so every product is exact in
+//     fp32. 2^e is one power of two per KV head that brings max |d_v| into
+//     [1, 2): it keeps A clear of fp16 subnormals and overflow, and l is scaled
+//     by the same factor.
+//   A masked key contributes exactly 0 even over NaN/Inf block scales (as ggml's
+//   CPU loop, which skips it): a -inf mask entry replaces the logit, and the
+//   pre-pass reads NaN/Inf V scales as 0.
 // Computing S^T (keys as rows) leaves each lane with 8 logits of one query row
 // in the A-operand layout of the P*V MFMA. K rows sit in LDS in the order
 // r -> key sigma(r) = 8*((r>>2)&3) + 4*(r>>4) + (r&3), which makes a lane's 8
@@ -86,6 +88,8 @@ constexpr int kLdsA = kLdsP + 2 * kPBuf;          // [4 waves][2 rg][16 rows] f3
 constexpr int kABuf = kScoreWaves * kRG * 16 * 4;
 constexpr int kLdsMask = kLdsA + 2 * kABuf;       // [qb positions][32 keys] f16
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kSlack = 8.0f;  // log2 of the largest P the lazy rescale admits
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 static_assert(kTileBytes == 49664 && kTileBytes % 256 == 0, "tile record");
 constexpr int kLdsMaxBytes = kLdsMask + 2 * 128 * kPK * 2;  // with the mask stages of G = 1
@@ -211,9 +215,10 @@ __global__ __launch_bounds__(256) void kvprep_kernel(const uint8_t *__restrict__
 #pragma unroll
             for (int kk = 0; kk < 32; ++kk) {
                 dd[kk] = *reinterpret_cast<const uint16_t *>(sv + kHeadRowBytes * (32 * u + kk) + 18 * b);
-                // the largest finite |d_v| sets the power of two applied to P d_v; a
-                // NaN/Inf scale (bytes that are not q4_0) stays out of it
-                const uint32_t mag = (dd[kk] & 0x7C00u) == 0x7C00u ? 0u : (dd[kk] & 0x7fffu);
+                // a NaN/Inf scale (bytes that are not q4_0) reads as 0: such a key, if
+                // masked, adds exactly 0 (P d_v is formed in fp16, where 0 * NaN = NaN)
+                dd[kk] = (dd[kk] & 0x7C00u) == 0x7C00u ? (uint16_t)0 : dd[kk];
+                const uint32_t mag = dd[kk] & 0x7fffu;
                 dmax = mag > dmax ? mag : dmax;
             }
             uint8_t *vrec = kv + ((int64_t)h * kv_tiles + ((k0 >> 5) + u)) * kTileBytes + kKHalf;
@@ -413,14 +418,15 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
     };
     if (n_tiles > 0) issue(0, -1);
 
-    // e with max |d_v| * 2^e in [1, 2); P carries 2^e (added to the exponent)
-    float eshift = 0.0f;
+    // e with max |d_v| * 2^e in [1, 2) (at most 2^15, the largest power of two in
+    // fp16): the value waves scale d_v by 2^e, l carries the same factor
+    int e2 = 0;
     {
         const float dm = h2f(p.dvmax[kvh]);
         if (dm > 0.0f) {
             int e;
             (void)frexpf(dm, &e);
-            eshift = (float)(1 - e);
+            e2 = 1 - e < 15 ? 1 - e : 15;
         }
     }
     const int nh = (n >> 3) & 1;
@@ -548,10 +554,13 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             float *ab = reinterpret_cast<float *>(smem + kLdsA + (t & 1) * kABuf) + w * (kRG * 16);
 #pragma unroll
             for (int rg = 0; rg < kRG; ++rg) {
+                // lazy maximum: the reference moves only when a logit passes it by more
+                // than kSlack, so P <= 2^kSlack and most tiles need no rescale of O
                 float alpha = 1.0f;
                 bool over = false;
+                const float lim = m_run[rg] + kSlack;
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) over |= s[rg][jj] > m_run[rg];
+                for (int jj = 0; jj < 8; ++jj) over |= s[rg][jj] > lim;
                 if (__any(over)) {
                     float mt = fmaxf(fmaxf(fmaxf(s[rg][0], s[rg][1]), fmaxf(s[rg][2], s[rg][3])),
                                      fmaxf(fmaxf(s[rg][4], s[rg][5]), fmaxf(s[rg][6], s[rg][7])));
@@ -562,7 +571,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                     l_part[rg] *= alpha;
                     m_run[rg] = m_new;
                 }
-                const float mref = (m_run[rg] == -INFINITY ? 0.0f : m_run[rg]) - eshift;
+                const float mref = m_run[rg] == -INFINITY ? 0.0f : m_run[rg];
                 float pf[8], psum = 0.0f;
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj) {
@@ -570,8 +579,15 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                     psum += pf[jj];
                 }
                 l_part[rg] += psum;
-                *reinterpret_cast<float4 *>(pb + rg * 2048) = make_float4(pf[0], pf[1], pf[2], pf[3]);
-                *reinterpret_cast<float4 *>(pb + rg * 2048 + 1024) = make_float4(pf[4], pf[5], pf[6], pf[7]);
+                // P as an fp16 hi + lo pair (22 bits): the value waves form P d_v from it
+                half8 ph, pl;
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    ph[jj] = (_Float16)pf[jj];
+                    pl[jj] = (_Float16)(pf[jj] - (float)ph[jj]);
+                }
+                *reinterpret_cast<half8 *>(pb + rg * 2048) = ph;
+                *reinterpret_cast<half8 *>(pb + rg * 2048 + 1024) = pl;
                 if (g == 0) ab[rg * 16 + n] = alpha;
             }
         }
@@ -600,6 +616,9 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
     const int v_off0 = 64 * n + 16 * (g ^ ((n >> 1) & 3)) + 8 * nh;
     const int v_off1 = v_off0 ^ 8;
     const int p_off = w * (kRG * 2048) + 16 * lane;
+    const _Float16 d2e_s = (_Float16)ldexpf(1.0f, e2);
+    const half8 d2e = {d2e_s, d2e_s, d2e_s, d2e_s, d2e_s, d2e_s, d2e_s, d2e_s};
+    const float l_scale = ldexpf(1.0f, e2);  // O carries 2^e: l gets it too
     floatx4 acc[kRG][16];
 #pragma unroll
     for (int rg = 0; rg < kRG; ++rg)
@@ -616,15 +635,23 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
         asm volatile("" : "+v"(vb0), "+v"(vb1));
         const uint8_t *pb = smem + kLdsP + (tp & 1) * kPBuf + p_off;
         const float *ab = reinterpret_cast<const float *>(smem + kLdsA + (tp & 1) * kABuf) + w * (kRG * 16);
-        float pf[kRG][8];
-        floatx4 a4[kRG];  // rescale factors of rows 4g..4g+3 (exactly 1 where no maximum grew)
+        half8 ph[kRG], pl[kRG];
+        bool resc = false;
 #pragma unroll
         for (int rg = 0; rg < kRG; ++rg) {
-            a4[rg] = *reinterpret_cast<const floatx4 *>(ab + rg * 16 + 4 * g);
-            const float4 p0 = *reinterpret_cast<const float4 *>(pb + rg * 2048);
-            const float4 p1 = *reinterpret_cast<const float4 *>(pb + rg * 2048 + 1024);
-            pf[rg][0] = p0.x; pf[rg][1] = p0.y; pf[rg][2] = p0.z; pf[rg][3] = p0.w;
-            pf[rg][4] = p1.x; pf[rg][5] = p1.y; pf[rg][6] = p1.z; pf[rg][7] = p1.w;
+            // rescale factors of rows 4g..4g+3: exactly 1 unless a maximum moved
+            const floatx4 a4 = *reinterpret_cast<const floatx4 *>(ab + rg * 16 + 4 * g);
+            resc |= (a4[0] != 1.0f) | (a4[1] != 1.0f) | (a4[2] != 1.0f) | (a4[3] != 1.0f);
+            ph[rg] = *reinterpret_cast<const half8 *>(pb + rg * 2048);
+            pl[rg] = *reinterpret_cast<const half8 *>(pb + rg * 2048 + 1024);
+        }
+        if (__any(resc)) {  // rare with the lazy maximum: O = alpha O
+#pragma unroll
+            for (int rg = 0; rg < kRG; ++rg) {
+                const floatx4 a4 = *reinterpret_cast<const floatx4 *>(ab + rg * 16 + 4 * g);
+#pragma unroll
+                for (int T = 0; T < 16; ++T) acc[rg][T] *= a4;
+            }
         }
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
@@ -633,6 +660,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                 const uint4 u = *reinterpret_cast<const uint4 *>(vs + kOffDv + 64 * b + 16 * g);
                 __builtin_memcpy(&dvb, &u, 16);
             }
+            dvb *= d2e;  // d_v 2^e, exact (a power of two, |d_v| 2^e < 2)
             // A = P 2^e d_v as an fp16 hi + lo pair (22 bits): the products with the
             // exact V codes are then exact in fp32, so a row that a few keys
             // dominate carries no fp16 rounding of P d_v into its output.
@@ -641,23 +669,16 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             for (int hf = 0; hf < 2; ++hf) bv[hf] = lds_half8(smem, vb0 + 1024 * (2 * b + hf), vb1 + 1024 * (2 * b + hf));
 #pragma unroll
             for (int rg = 0; rg < kRG; ++rg) {
-                half8 a, al;
-#pragma unroll
-                for (int jj = 0; jj < 8; ++jj) {
-                    // 0 * x = 0 for every x (v_mul_legacy): a key with P = 0 adds
-                    // exactly 0 whatever its V scale holds
-                    float x;
-                    asm("v_mul_legacy_f32 %0, %1, %2" : "=v"(x) : "v"(pf[rg][jj]), "v"((float)dvb[jj]));
-                    a[jj] = (_Float16)x;
-                    al[jj] = (_Float16)(x - (float)a[jj]);
-                }
-                // O = alpha O + P V; the product is applied unconditionally (exact
-                // for alpha = 1): a conditional rescale makes the compiler keep a
-                // second copy of O and spill
+                // A = P d_v 2^e as hi + lo in packed fp16: Ph d_v has at most 22
+                // significant bits, so its residual after rounding to fp16 (at most
+                // 11 bits) is exact in one fma; Pl d_v is 2^-11 of it and rounds once
+                const half8 a = ph[rg] * dvb;
+                const half8 r = __builtin_elementwise_fma(ph[rg], dvb, -a);
+                const half8 al = __builtin_elementwise_fma(pl[rg], dvb, r);
 #pragma unroll
                 for (int hf = 0; hf < 2; ++hf) {
                     const int T = 2 * b + hf;
-                    acc[rg][T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv[hf], acc[rg][T] * a4[rg], 0, 0, 0);
+                    acc[rg][T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv[hf], acc[rg][T], 0, 0, 0);
                     acc[rg][T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv[hf], acc[rg][T], 0, 0, 0);
                 }
             }
@@ -674,7 +695,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             const int qrow = q_base + r / p.G, hrow = kvh * p.G + r % p.G;
             if (qrow >= p.n_q) continue;
             const float mrow = n_tiles > 0 ? ml[rg * 32 + 2 * (4 * g + i)] : -INFINITY;
-            const float lrow = n_tiles > 0 ? ml[rg * 32 + 2 * (4 * g + i) + 1] : 0.0f;
+            const float lrow = n_tiles > 0 ? ml[rg * 32 + 2 * (4 * g + i) + 1] * l_scale : 0.0f;
             const int64_t ridx = (int64_t)qrow * p.H + hrow;
             if (p.n_splits == 1) {
                 const float inv = lrow == 0.0f ? 0.0f : 1.0f / lrow;
