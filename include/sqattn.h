@@ -178,6 +178,24 @@ int sqa_supports_flash_attn_ext(const sqa_tensor *q, const sqa_tensor *k, const 
                                 float logit_softcap, const sqa_tensor *dst);
 
 /*
+ * Allocation-free form of sqa_flash_attn_ext for decode/verify shapes (up to 4
+ * positions and 16 query rows per KV head, 2 KV heads, 16-byte aligned q rows).
+ * It has no counterpart in the reference: it is for callers that cannot
+ * allocate or pass a workspace (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Its scratch is a device array of
+ * SQA_STATIC_SCRATCH_BYTES inside the library, one per GPU, held until the
+ * process ends; no call allocates or frees memory. Every call on one GPU
+ * shares that GPU's array, so calls that overlap on one GPU (two streams, two
+ * threads) race. Shapes whose scratch exceeds the maximum return
+ * SQA_ERR_WORKSPACE, other shapes SQA_ERR_UNSUPPORTED. Same arguments, result
+ * and errors as sqa_flash_attn_ext otherwise.
+ */
+#define SQA_STATIC_SCRATCH_BYTES (16u << 20)
+int sqa_flash_attn_ext_static(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
+                              const sqa_tensor *mask, float scale, float max_bias, float logit_softcap,
+                              const sqa_tensor *dst, void *stream);
+
+/*
  * Mask-free causal variant with an optional fused output gate. Query t sits at
  * absolute position q_pos0 + t and sees keys 0..q_pos0+t, the rule the engine
  * encodes in its host-built F16 mask (reference: src/model/graph.rs:486-576,

@@ -19,7 +19,7 @@ import torch
 
 __all__ = [
     "Tensor", "lib", "last_error", "SqaError", "set_rows_q4_0", "flash_attn_ext",
-    "flash_attn_ext_causal", "sigmoid_mul", "fill_causal_mask", "supports_flash_attn_ext",
+    "flash_attn_ext_causal", "flash_attn_ext_static", "sigmoid_mul", "fill_causal_mask", "supports_flash_attn_ext",
     "flash_attn_workspace_size", "KvCache", "cache_view", "row_bytes", "profile_begin", "profile_end",
     "profile_get", "Rope", "rope_params", "rope_norm_set_rows_q4_0", "rope_norm_f32",
 ]
@@ -115,6 +115,7 @@ def lib():
             "sqa_flash_attn_ext_workspace_size": (sz, [P, P, P, P]),
             "sqa_supports_flash_attn_ext": (ctypes.c_int, [P, P, P, P, f32, f32, f32, P]),
             "sqa_flash_attn_ext_causal": (ctypes.c_int, [P, P, P, i64, P, f32, P, vp, sz, vp]),
+            "sqa_flash_attn_ext_static": (ctypes.c_int, [P, P, P, P, f32, f32, f32, P, vp]),
             "sqa_sigmoid_mul": (ctypes.c_int, [P, P, P, vp]),
             "sqa_fill_causal_mask": (ctypes.c_int, [P, i64, vp]),
             "sqa_kv_cache_layer_bytes": (sz, [i64, i64, i64]),
@@ -293,6 +294,21 @@ def flash_attn_ext(q, k_cache, v_cache, n_kv, mask=None, scale=None, max_bias=0.
     wbytes = workspace.numel() if workspace is not None else 0
     _check(lib().sqa_flash_attn_ext(ctypes.byref(tq), ctypes.byref(tk), ctypes.byref(tv), _ref(tm), scale,
                                     max_bias, softcap, ctypes.byref(to), wptr, wbytes, _stream(stream)))
+    return out
+
+
+def flash_attn_ext_static(q, k_cache, v_cache, n_kv, mask=None, scale=None, max_bias=0.0, softcap=0.0,
+                          out=None, stream=None):
+    """flash_attn_ext for decode/verify shapes with the library's own device scratch:
+    no workspace, no allocation inside the call (out must be given for that)."""
+    n_q, H, D = q.shape
+    scale = D ** -0.5 if scale is None else scale
+    if out is None:
+        out = torch.empty((n_q, H, D), dtype=torch.float32, device=q.device)
+    tq, tk, tv = q_desc(q), cache_view(k_cache, n_kv), cache_view(v_cache, n_kv)
+    to, tm = out_desc(out), mask_desc(mask)
+    _check(lib().sqa_flash_attn_ext_static(ctypes.byref(tq), ctypes.byref(tk), ctypes.byref(tv), _ref(tm), scale,
+                                           max_bias, softcap, ctypes.byref(to), _stream(stream)))
     return out
 
 

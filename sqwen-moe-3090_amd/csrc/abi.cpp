@@ -300,6 +300,36 @@ int sqa_flash_attn_ext(const sqa_tensor *q, const sqa_tensor *k, const sqa_tenso
     return run_fa(a, decode, (hipStream_t)stream);
 }
 
+int sqa_flash_attn_ext_static(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
+                              const sqa_tensor *mask, float scale, float max_bias, float logit_softcap,
+                              const sqa_tensor *dst, void *stream) {
+    bool decode = false;
+    int rc = check_fa(q, k, v, dst, &decode);
+    if (rc) return rc;
+    rc = check_mask(mask, q, k);
+    if (rc) return rc;
+    if (!isfinite(scale)) return set_error(SQA_ERR_INVALID, "flash_attn_ext_static: scale not finite");
+    if (max_bias != 0.0f)
+        return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext_static: ALiBi (max_bias != 0) not supported");
+    if (logit_softcap != 0.0f)
+        return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext_static: logit_softcap not supported");
+    if (!decode)
+        return set_error(SQA_ERR_UNSUPPORTED,
+                         "flash_attn_ext_static: only decode/verify shapes (up to 4 positions and 16 query "
+                         "rows per KV head, 2 KV heads, 16-byte aligned q rows); use sqa_flash_attn_ext");
+    const size_t need = fa_decode_workspace(q->ne[1], q->ne[2], k->ne[1]);
+    if (need > kStaticScratchBytes)
+        return set_error(SQA_ERR_WORKSPACE,
+                         "flash_attn_ext_static: these shapes need %zu bytes of scratch, above its %zu-byte "
+                         "maximum; use sqa_flash_attn_ext with a workspace",
+                         need, kStaticScratchBytes);
+    void *ws = nullptr;
+    rc = static_scratch(&ws);
+    if (rc) return rc;
+    FaArgs a{q, k, v, mask, nullptr, dst, scale, -1, ws, kStaticScratchBytes};
+    return launch_fa_decode(a, (hipStream_t)stream);
+}
+
 int sqa_flash_attn_ext_causal(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
                               int64_t q_pos0, const sqa_tensor *gate, float scale,
                               const sqa_tensor *dst, void *workspace, size_t workspace_bytes,

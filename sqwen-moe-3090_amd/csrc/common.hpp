@@ -47,6 +47,10 @@ struct FaArgs {
     size_t ws_bytes;
 };
 size_t fa_decode_workspace(int64_t n_q, int64_t H, int64_t n_kv);
+// Device scratch of the allocation-free decode entry point: its size, and its
+// address on the current device (looked up once per device).
+constexpr size_t kStaticScratchBytes = SQA_STATIC_SCRATCH_BYTES;
+int static_scratch(void **out);
 // Merges split partials [n_splits][rows][256] + [n_splits][rows][2] into dst;
 // n_splits <= kMaxSplits (the split planners cap there).
 constexpr int kMaxSplits = 256;

@@ -65,6 +65,7 @@
 //   16x16x64 i8 : A[n][16g..16g+15]  B[16g..16g+15][n]  C[4g..4g+3][n]
 //   16x16x32 f16: A[n][8g..8g+7]     B[8g..8g+7][n]     C[4g..4g+3][n]
 #include <mutex>
+#include <vector>
 
 #include "common.hpp"
 
@@ -773,6 +774,32 @@ int decode_splits(int64_t n_kv) {
 size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 }  // namespace
+
+// Scratch of the allocation-free decode entry point (sqa_flash_attn_ext_static):
+// split partials and, for an unaligned mask, its packed copy. A file-scope
+// device array: every GPU the library runs on holds its own copy at its own
+// address until the process ends, and every call on that GPU shares it, so
+// calls that overlap on one GPU race. Host code takes its address per device
+// from hipGetSymbolAddress and never uses the array's name as a device pointer.
+__device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+int static_scratch(void **out) {
+    static std::mutex mu;
+    static std::vector<void *> ptrs;  // per device
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "flash_attn_ext_static: hipGetDevice");
+    std::lock_guard<std::mutex> lock(mu);
+    if ((int)ptrs.size() <= dev) ptrs.resize(dev + 1, nullptr);
+    if (!ptrs[dev]) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e, "flash_attn_ext_static: hipGetSymbolAddress(scratch)");
+        ptrs[dev] = ptr;
+    }
+    *out = ptrs[dev];
+    return SQA_OK;
+}
 
 size_t fa_decode_workspace(int64_t n_q, int64_t H, int64_t n_kv) {
     const int64_t splits = decode_splits(n_kv);
