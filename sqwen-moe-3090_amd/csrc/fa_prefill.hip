@@ -3,16 +3,16 @@
 // src/model/attn.rs:228-251 in the reference (n_q = 512 or 2048 over a q4_0
 // cache of 16K-133K keys).
 //
-// Three short pre-passes, then one MFMA kernel:
-//   kdeq  K q4_0 -> per 32-key tile: Kh, Kl fp16 [32 keys][256] with
-//                 x = (nib-8)*d = Kh + Kl exactly (x has <= 14 significant
-//                 bits, Kh + Kl hold 22)
-//   vdeq  V q4_0 -> per tile: Vc fp16 codes [256 dims][32 keys] and Dv fp16
-//                 scales [8 blocks][32 keys]; per KV head the largest |d_v|
-//   qprep Q f32  -> q8_0 with ggml's x86 rounding (d = amax/127, codes =
-//                 rint(x * 127/amax)): codes as fp16 integers [n_q*H][256] and
-//                 fp16(d) * scale * log2(e) as f32 [n_q*H][8]
-// A tile of one KV head is a contiguous 49664-byte record [Kh | Kl | Vc | Dv]
+// Two short pre-passes, then one MFMA kernel:
+//   kvprep K, V q4_0 -> per 32-key tile and KV head: Kc fp16 codes (nib - 8)
+//                 [32 keys][256] and Dk fp16 scales [8 blocks][32 keys]; Vc
+//                 fp16 codes [256 dims][32 keys] and Dv fp16 scales [8 blocks]
+//                 [32 keys]; per KV head the largest |d_v|
+//   qprep  Q f32 -> q8_0 with ggml's x86 rounding (d = amax/127, codes =
+//                 rint(x * 127/amax)), then Q' = code * fp16(d) * scale *
+//                 log2(e) as an fp16 hi + lo pair [n_q*H][256] each (Q' has at
+//                 most 7 + 24 significant bits; hi + lo hold 22 of them)
+// A tile of one KV head is a contiguous 33792-byte record [Kc | Dk | Vc | Dv]
 // laid out exactly as the main kernel wants it in LDS (rows permuted, chunks
 // swizzled, see below), so its K and V halves move HBM -> LDS as straight
 // copies. Keys past n_kv are zero.
@@ -20,10 +20,11 @@
 // fa_prefill_kernel: a workgroup takes 128 query rows of ONE KV head (GQA
 // packed: row r is position r / G, head kvh*G + r % G) and streams 32-key
 // tiles. Its 8 wavefronts (2 per SIMD) split the work by kind:
-//   score wave w (0..3), rows 32w..32w+31, holds their Q codes (64 registers):
-//     S^T = sum over q4_0 blocks b of d_q[b] * (Kh_b.q_b + Kl_b.q_b), the
-//     products on v_mfma_f32_16x16x32_f16 (all exact in fp32) and the d_q
-//     scaling (with scale * log2 e) as an fp32 FMA; then the mask and the
+//   score wave w (0..3), rows 32w..32w+31, holds their Q' hi and lo (128
+//     registers): S^T = sum over q4_0 blocks b of d_k[b] * (Kc_b.Q'h_b +
+//     Kc_b.Q'l_b), the products on v_mfma_f32_16x16x32_f16 (all exact in
+//     fp32: a code has at most 3 significant bits) and the d_k scaling as an
+//     fp32 FMA with the fp16 scale as operand; then the mask and the
 //     online softmax in fp32 (base 2, with a lazy reference maximum that moves
 //     only when a logit passes it by more than 2^8, so P <= 2^8 and most tiles
 //     need no rescale of O). P (as an fp16 hi + lo pair) and the rescale
@@ -72,14 +73,14 @@ constexpr int kWaves = kScoreWaves + kValueWaves;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kRG = 2;                   // 16-row groups per score wave
 constexpr int kRowsPerWG = kScoreWaves * kRG * 16;  // 128 query rows
-constexpr int kOffKl = kPK * 512;        // inside the K half: Kl after Kh
-constexpr int kKHalf = 2 * kOffKl;       // Kh + Kl: 32768 bytes
+constexpr int kOffDk = kPK * 512;        // inside the K half: Dk after Kc
+constexpr int kKHalf = kOffDk + 8 * kPK * 2;  // Kc + Dk: 16896 bytes
 constexpr int kOffDv = kHeadDim * kPK * 2;  // inside the V half: Dv after Vc
 constexpr int kVHalf = kOffDv + 8 * kPK * 2;  // Vc + Dv: 16896 bytes
 constexpr int kTileBytes = kKHalf + kVHalf;   // one tile record
-constexpr int kKInst = kKHalf / 1024;    // 32 DMA instructions
+constexpr int kKInst = (kKHalf + 1023) / 1024;  // 17 DMA instructions, the last one 512 bytes
 constexpr int kVInst = (kVHalf + 1023) / 1024;  // 17, the last one 512 bytes
-constexpr int kKStage = kKHalf, kVStage = kVInst * 1024;
+constexpr int kKStage = kKInst * 1024, kVStage = kVInst * 1024;
 // LDS map: 2 K stages | 2 V stages | 2 P buffers | 2 rescale buffers | 2 mask stages
 constexpr int kLdsV = 2 * kKStage;
 constexpr int kLdsP = kLdsV + 2 * kVStage;        // [4 waves][2 rg][2 halves][64 lanes][16 B]
@@ -91,7 +92,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kSlack = 8.0f;  // log2 of the largest P the lazy rescale admits
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
-static_assert(kTileBytes == 49664 && kTileBytes % 256 == 0, "tile record");
+static_assert(kTileBytes == 33792 && kTileBytes % 256 == 0, "tile record");
+static_assert(kKHalf == kVHalf && kKInst == 17 && kVInst == 17, "both halves: 16 DMA instructions and a half");
 constexpr int kLdsMaxBytes = kLdsMask + 2 * 128 * kPK * 2;  // with the mask stages of G = 1
 static_assert(kLdsMaxBytes <= 160 * 1024, "LDS budget");
 
@@ -122,18 +124,11 @@ __device__ __forceinline__ int key_row(int k) { return 16 * ((k >> 2) & 1) + 4 *
 
 // ---------------------------------------------------------------- pre-passes
 
-// x -> (hi, lo) fp16 bit patterns with hi + lo == x for x of <= 22 significant bits.
-__device__ __forceinline__ void split_hl(float x, uint16_t &hi, uint16_t &lo) {
-    const _Float16 h = (_Float16)x;
-    const _Float16 l = (_Float16)(x - (float)h);
-    __builtin_memcpy(&hi, &h, 2);
-    __builtin_memcpy(&lo, &l, 2);
-}
-
 // One workgroup per (64 keys, KV head): the 64 q4_0 rows of K and of V are
 // staged in LDS with 16-byte loads (zeros past n_kv), then
 //   K: thread t takes blocks (key, b) = t and t + 256 (key = idx / 8, b = idx % 8):
-//      32 fp16 Kh + 32 fp16 Kl as 4 + 4 swizzled 16-byte chunks of the key's row;
+//      its 32 codes as fp16 (4 swizzled 16-byte chunks of the key's row) and its
+//      scale into the Dk row of block b;
 //   V: thread t writes the Vc row of dim t (32 codes, 64 bytes) of both tiles;
 //      threads 0..15 write the Dv rows and fold the largest |d_v| into
 //      dvmax[head] (fp16 magnitude bits, cleared by qprep_kernel, which runs
@@ -162,29 +157,30 @@ __global__ __launch_bounds__(256) void kvprep_kernel(const uint8_t *__restrict__
         const int idx = t + 256 * i;
         const int key = idx >> 3, b = idx & 7;
         const uint16_t *src = reinterpret_cast<const uint16_t *>(sk + kHeadRowBytes * key + 18 * b);
-        const float d = h2f(src[0]);
-        uint16_t out[32], outl[32];
+        uint16_t out[32];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint32_t two = src[1 + j];  // qs[2j], qs[2j+1]
             const int b0 = two & 0xff, b1 = two >> 8;
-            split_hl((float)((b0 & 15) - 8) * d, out[2 * j], outl[2 * j]);
-            split_hl((float)((b1 & 15) - 8) * d, out[2 * j + 1], outl[2 * j + 1]);
-            split_hl((float)((b0 >> 4) - 8) * d, out[16 + 2 * j], outl[16 + 2 * j]);
-            split_hl((float)((b1 >> 4) - 8) * d, out[16 + 2 * j + 1], outl[16 + 2 * j + 1]);
+            const _Float16 c0 = (_Float16)((b0 & 15) - 8), c1 = (_Float16)((b1 & 15) - 8);
+            const _Float16 c2 = (_Float16)((b0 >> 4) - 8), c3 = (_Float16)((b1 >> 4) - 8);
+            __builtin_memcpy(&out[2 * j], &c0, 2);
+            __builtin_memcpy(&out[2 * j + 1], &c1, 2);
+            __builtin_memcpy(&out[16 + 2 * j], &c2, 2);
+            __builtin_memcpy(&out[16 + 2 * j + 1], &c3, 2);
         }
         const int64_t gkey = k0 + key;
         const int r = key_row((int)(gkey & (kPK - 1)));
-        uint8_t *row = kv + ((int64_t)h * kv_tiles + (gkey >> 5)) * kTileBytes + r * 512;
+        uint8_t *rec = kv + ((int64_t)h * kv_tiles + (gkey >> 5)) * kTileBytes;
+        uint8_t *row = rec + r * 512;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int pos = (4 * b + j) ^ (r & 7);
-            uint4 x, y;
+            uint4 x;
             __builtin_memcpy(&x, out + 8 * j, 16);
-            __builtin_memcpy(&y, outl + 8 * j, 16);
             *reinterpret_cast<uint4 *>(row + 16 * pos) = swap_halves(x, r & 8);
-            *reinterpret_cast<uint4 *>(row + kOffKl + 16 * pos) = swap_halves(y, r & 8);
         }
+        *reinterpret_cast<uint16_t *>(rec + kOffDk + (b * kPK + r) * 2) = src[0];
     }
     // V: thread t writes the Vc row of dim t (its 32 keys' codes, 64 bytes) of
     // both tiles; threads 0..15 also write the Dv row of (tile t / 8, block t % 8)
@@ -241,11 +237,12 @@ __global__ __launch_bounds__(256) void kvprep_kernel(const uint8_t *__restrict__
 }
 
 // One thread per 32-value block of one (query, head) row: q8_0 with ggml's x86
-// rounding (d = amax/127, codes = rint(x * 127/amax)); the codes as fp16
-// (exact integers) and fp16(d) * scale * log2(e) as f32.
+// rounding (d = amax/127, codes = rint(x * 127/amax)), then Q' = code * qd with
+// qd = fp16(d) * scale * log2(e) in fp32, written as fp16 hi = fp16(Q') and
+// lo = fp16(Q' - hi).
 __global__ __launch_bounds__(256) void qprep_kernel(const char *__restrict__ q, int64_t nb1, int64_t nb2,
-                                                    int n_q, int H, float qscale, uint16_t *__restrict__ qc,
-                                                    float *__restrict__ qd, uint32_t *__restrict__ dvmax, int hkv,
+                                                    int n_q, int H, float qscale, uint16_t *__restrict__ qh,
+                                                    uint16_t *__restrict__ ql, uint32_t *__restrict__ dvmax, int hkv,
                                                     bool aligned) {
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (gid < hkv) dvmax[gid] = 0;  // for kvprep_kernel, launched next
@@ -271,20 +268,30 @@ __global__ __launch_bounds__(256) void qprep_kernel(const char *__restrict__ q, 
     for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
     const float d = amax / 127.f;
     const float id = amax != 0.0f ? 127.f / amax : 0.0f;
-    uint16_t oc[32];
+    const float qd = (float)(_Float16)d * qscale;
+    uint16_t oh[32], ol[32];
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
-        const _Float16 cv = (_Float16)rintf(v[j] * id);
-        __builtin_memcpy(&oc[j], &cv, 2);
+        // x opaque: left visible, the compiler may round code * qd to fp16 twice
+        // (once from the fp32 product for hi, once from the exact product for the
+        // hi it subtracts), and a hi + lo off by one fp16 ulp of hi
+        float x = rintf(v[j] * id) * qd;
+        asm volatile("" : "+v"(x));
+        const _Float16 h = (_Float16)x;
+        const _Float16 l = (_Float16)(x - (float)h);
+        __builtin_memcpy(&oh[j], &h, 2);
+        __builtin_memcpy(&ol[j], &l, 2);
     }
-    uint4 *dc4 = reinterpret_cast<uint4 *>(qc + row * kHeadDim + 32 * b);
+    uint4 *h4 = reinterpret_cast<uint4 *>(qh + row * kHeadDim + 32 * b);
+    uint4 *l4 = reinterpret_cast<uint4 *>(ql + row * kHeadDim + 32 * b);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        uint4 a;
-        __builtin_memcpy(&a, oc + 8 * j, 16);
-        dc4[j] = a;
+        uint4 a, c;
+        __builtin_memcpy(&a, oh + 8 * j, 16);
+        __builtin_memcpy(&c, ol + 8 * j, 16);
+        h4[j] = a;
+        l4[j] = c;
     }
-    qd[row * kBlocksPerHead + b] = (float)(_Float16)d * qscale;
 }
 
 // Copies an F16 mask whose rows are unaligned or whose length is not a
@@ -325,8 +332,7 @@ __device__ __forceinline__ half8 lds_half8(const uint8_t *base, int off_lo, int 
 struct PrefillParams {
     const uint8_t *kv;        // [Hkv][kv_tiles] tile records
     const uint32_t *dvmax;    // [Hkv] fp16 magnitude bits
-    const uint16_t *qc;       // [n_q*H][256] fp16 codes
-    const float *qd;          // [n_q*H][8]
+    const uint16_t *qh, *ql;  // [n_q*H][256] fp16 Q' hi and lo
     int64_t n_kv, kv_tiles;
     int n_q, H, G, Hkv;
     const char *mask;  // F16 rows 16-byte aligned, mask_len (a multiple of 8) keys each, or null
@@ -374,8 +380,8 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
 
     // ---------------- DMA: 1 KB per instruction, a fixed share per wave ---------
     // Iteration t: K half + mask of tile t + 1, V half of tile t (stage = tile & 1).
-    // K instruction jj (0..31) goes to wave jj % 8, V instruction jj (0..16, the
-    // last one 512 bytes) to wave (jj + 4) % 8, mask instruction jm (< 8) to wave
+    // K instruction jj (0..16, the last one 512 bytes) goes to wave jj % 8, V
+    // instruction jj to wave (jj + 4) % 8, mask instruction jm (< 8) to wave
     // (jm + 2) % 8.
     const int n_mask_inst = p.mask ? (p.qb + 15) / 16 : 0;
     const uint8_t *kv_h = p.kv + (int64_t)kvh * p.kv_tiles * kTileBytes;
@@ -394,9 +400,10 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             const uint8_t *rec = kv_h + (kt / kPK) * kTileBytes;
             const uint32_t st = lds0 + (uint32_t)((t_k & 1) * kKStage);
 #pragma unroll
-            for (int i = 0; i < kKInst / kWaves; ++i) {
+            for (int i = 0; i < 3; ++i) {
                 const int jj = jk0 + kWaves * i;
-                dma16(1024u * jj + 16u * lane, rec, st + 1024u * jj);
+                if (jj < kKInst - 1 || (jj == kKInst - 1 && lane < 32))
+                    dma16(1024u * jj + 16u * lane, rec, st + 1024u * jj);
             }
             if (has_m) {
                 const int64_t col = kt + 8 * m_c < p.mask_len ? kt + 8 * m_c : p.mask_len - 8;
@@ -436,10 +443,9 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
     if (wave < kScoreWaves) {
         const int w = wave;
         float *ml = reinterpret_cast<float *>(smem + kLdsP) + w * (kRG * 32);  // [rg][row][m, l]
-        // Q codes of rows r = 32w + 16rg + n (position q_base + r / G, head
-        // kvh*G + r % G) as B operands, dims 32b + 8g..+7, and their d_q
-        half8 bq[kRG][8];
-        float qd[kRG][8];
+        // Q' hi and lo of rows r = 32w + 16rg + n (position q_base + r / G, head
+        // kvh*G + r % G) as B operands, dims 32b + 8g..+7
+        half8 bqh[kRG][8], bql[kRG][8];
         int my_pos[kRG], m_off[kRG];
         float m_run[kRG], l_part[kRG];
 #pragma unroll
@@ -452,14 +458,13 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             const int64_t row = (int64_t)(ok ? pos : 0) * p.H + kvh * p.G + r % p.G;
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
-                uint4 u = *reinterpret_cast<const uint4 *>(p.qc + row * kHeadDim + 32 * b + 8 * g);
+                uint4 u = *reinterpret_cast<const uint4 *>(p.qh + row * kHeadDim + 32 * b + 8 * g);
+                uint4 v = *reinterpret_cast<const uint4 *>(p.ql + row * kHeadDim + 32 * b + 8 * g);
                 u = make_uint4(u.x & m, u.y & m, u.z & m, u.w & m);
-                __builtin_memcpy(&bq[rg][b], &u, 16);
+                v = make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+                __builtin_memcpy(&bqh[rg][b], &u, 16);
+                __builtin_memcpy(&bql[rg][b], &v, 16);
             }
-            const float4 d0 = *reinterpret_cast<const float4 *>(p.qd + row * 8);
-            const float4 d1 = *reinterpret_cast<const float4 *>(p.qd + row * 8 + 4);
-            qd[rg][0] = d0.x; qd[rg][1] = d0.y; qd[rg][2] = d0.z; qd[rg][3] = d0.w;
-            qd[rg][4] = d1.x; qd[rg][5] = d1.y; qd[rg][6] = d1.z; qd[rg][7] = d1.w;
             const int pl = r / p.G;  // mask row of the position, keys 8g..8g+7
             m_off[rg] = kLdsMask + 64 * pl + 16 * (g ^ ((pl >> 1) & 3));
             m_run[rg] = -INFINITY;
@@ -505,19 +510,25 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             floatx4 sa[kRG][2];
 #pragma unroll
             for (int rg = 0; rg < kRG; ++rg) sa[rg][0] = sa[rg][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+            // d_k of the lane's four C rows 16kg + 4g + i, block b: 8 bytes at
+            // Dk[b][16kg + 4g]
+            const uint8_t *dkb = smem + (t & 1) * kKStage + kOffDk + 8 * g;
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
 #pragma unroll
                 for (int kg = 0; kg < 2; ++kg) {
                     const int o = kg * 8192 + 128 * (b >> 1);
-                    const half8 ah = lds_half8(smem, kb[b & 1][0] + o, kb[b & 1][1] + o);
-                    const half8 al = lds_half8(smem, kb[b & 1][0] + o + kOffKl, kb[b & 1][1] + o + kOffKl);
+                    const half8 ak = lds_half8(smem, kb[b & 1][0] + o, kb[b & 1][1] + o);
+                    const uint2 dk2 = *reinterpret_cast<const uint2 *>(dkb + 64 * b + 32 * kg);
+                    _Float16 dk[4];
+                    __builtin_memcpy(dk, &dk2, 8);
 #pragma unroll
                     for (int rg = 0; rg < kRG; ++rg) {
-                        floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq[rg][b],
+                        floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bqh[rg][b],
                                                                            floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq[rg][b], c, 0, 0, 0);
-                        sa[rg][kg] += qd[rg][b] * c;  // whole-vector: keeps sa one register tuple
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bql[rg][b], c, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) sa[rg][kg][i] = fmaf(c[i], (float)dk[i], sa[rg][kg][i]);
                     }
                 }
             }
@@ -731,7 +742,7 @@ struct PrefillPlan {
     int64_t kv_tiles;
     int qb, q_tiles, n_splits, mask_stage;
     int64_t split_len;
-    size_t off_kv, off_dvmax, off_qc, off_qd, off_mask, off_pa, off_pm, total;
+    size_t off_kv, off_dvmax, off_qh, off_ql, off_mask, off_pa, off_pm, total;
 };
 
 PrefillPlan plan(int64_t n_q, int64_t H, int64_t Hkv, int64_t n_kv) {
@@ -753,8 +764,8 @@ PrefillPlan plan(int64_t n_q, int64_t H, int64_t Hkv, int64_t n_kv) {
     size_t o = 0;
     pl.off_kv = o; o = al256(o + (size_t)Hkv * pl.kv_tiles * kTileBytes);
     pl.off_dvmax = o; o = al256(o + (size_t)Hkv * 4);
-    pl.off_qc = o; o = al256(o + (size_t)n_q * H * kHeadDim * 2);
-    pl.off_qd = o; o = al256(o + (size_t)n_q * H * 8 * 4);
+    pl.off_qh = o; o = al256(o + (size_t)n_q * H * kHeadDim * 2);
+    pl.off_ql = o; o = al256(o + (size_t)n_q * H * kHeadDim * 2);
     pl.off_mask = o; o = al256(o + (size_t)n_q * ((n_kv + 7) / 8 * 8) * 2);
     pl.off_pa = o;
     pl.off_pm = o;
@@ -785,8 +796,8 @@ int launch_fa_prefill(const FaArgs &a, hipStream_t s) {
     uint8_t *base = reinterpret_cast<uint8_t *>(((uintptr_t)a.ws + 255) & ~(uintptr_t)255);
     uint8_t *kv = base + pl.off_kv;
     uint32_t *dvmax = reinterpret_cast<uint32_t *>(base + pl.off_dvmax);
-    uint16_t *qc = reinterpret_cast<uint16_t *>(base + pl.off_qc);
-    float *qd = reinterpret_cast<float *>(base + pl.off_qd);
+    uint16_t *qh = reinterpret_cast<uint16_t *>(base + pl.off_qh);
+    uint16_t *ql = reinterpret_cast<uint16_t *>(base + pl.off_ql);
 
     PrefillParams p;
     p.mask = nullptr;
@@ -818,7 +829,7 @@ int launch_fa_prefill(const FaArgs &a, hipStream_t s) {
     {
         const int64_t nqb = n_q * H * kBlocksPerHead;
         qprep_kernel<<<dim3((unsigned)((nqb + 255) / 256)), dim3(256), 0, s>>>(
-            (const char *)q.data, (int64_t)q.nb[1], (int64_t)q.nb[2], (int)n_q, (int)H, a.scale * kLog2e, qc, qd,
+            (const char *)q.data, (int64_t)q.nb[1], (int64_t)q.nb[2], (int)n_q, (int)H, a.scale * kLog2e, qh, ql,
             dvmax, (int)Hkv, (uintptr_t)q.data % 16 == 0 && q.nb[1] % 16 == 0 && q.nb[2] % 16 == 0);
         kvprep_kernel<<<dim3((unsigned)(pl.kv_tiles / 2), (unsigned)Hkv), dim3(256), 0, s>>>(
             (const uint8_t *)k.data, (int64_t)k.nb[1], (int64_t)k.nb[2], (const uint8_t *)v.data, (int64_t)v.nb[1],
@@ -836,8 +847,8 @@ int launch_fa_prefill(const FaArgs &a, hipStream_t s) {
 
     p.kv = kv;
     p.dvmax = dvmax;
-    p.qc = qc;
-    p.qd = qd;
+    p.qh = qh;
+    p.ql = ql;
     p.n_kv = n_kv;
     p.kv_tiles = pl.kv_tiles;
     p.n_q = (int)n_q;
