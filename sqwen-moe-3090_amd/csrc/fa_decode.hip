@@ -11,7 +11,12 @@
 //   (so the cache lines the two heads share in a 288-byte row are fetched from
 //   HBM once and served to the second workgroup by that XCD's L2); two such
 //   workgroups fit on a CU, so one head's wavefronts can issue while the
-//   other's wait at their barrier. A workgroup (8 wavefronts) walks its split
+//   other's wait at their barrier. Of the two workgroups on a CU the one
+//   dispatched first wins the issue arbitration (older wavefronts go first)
+//   and runs about twice as fast while both are resident, so the splits of
+//   the first dispatch round take twice the tiles of the second: both rounds
+//   then end together (measured at 172K keys: 27.0 us against 28.6 us for
+//   equal splits, whose second round runs on alone for the last tiles). A workgroup (8 wavefronts) walks its split
 //   in 64-key tiles: four score wavefronts (16-key quarter w of every tile)
 //   compute the logits and the softmax weights P of tile t; four value
 //   wavefronts (64-dim slice v of the output) accumulate P V of tile t-1 over
@@ -109,6 +114,10 @@ constexpr float kSlack = 8.0f;  // log2 of the largest P the lazy rescale admits
 // P is stored as P 2^-kPShift (<= 2^(kSlack - kPShift) = 16) and l summed from the
 // same values, so A = P d_v stays below 65504 for every |d_v| < 4094.
 constexpr float kPShift = 4.0f;
+// Tile shares of a first-round and a second-round split when two workgroups
+// share each CU (see launch_fa_decode).
+constexpr int kFirstRoundWeight = 2;
+constexpr int kSecondRoundWeight = 1;
 static_assert(kTensorBytes % 1024 == 0, "a tile tensor must be whole DMA instructions");
 static_assert(2 * kLdsBytes <= 160 * 1024, "two workgroups per CU");
 static_assert(4 * 2 * 64 * 32 <= (kVStages - 1) * kTensorBytes, "Q operands must fit in V stages 1..2");
@@ -163,8 +172,11 @@ struct DecodeParams {
     int64_t n_kv;
     float qscale;           // softmax scale * log2(e)
     int n_splits;
-    int split_tiles;        // 64-key tiles of every split; the first split_extra splits take one more
-    int split_extra;
+    // Split s covers tiles [c(s) * tiles / cw_total, c(s + 1) * tiles / cw_total)
+    // with c(s) = w_first * s for s < n_first, else w_first * n_first +
+    // w_second * (s - n_first): a split of the first dispatch round weighs w_first.
+    int64_t tiles, cw_total;
+    int n_first, w_first, w_second;
     float *part_acc;        // [n_splits][n_q*H][256]
     float *part_ml;         // [n_splits][n_q*H][2]
 };
@@ -218,9 +230,14 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
     const int id = blockIdx.x;
     const int kvh = (id >> 3) & 1;
     const int split = ((id >> 4) << 3) | (id & 7);
-    const int t_begin = split * p.split_tiles + (split < p.split_extra ? split : p.split_extra);
-    const int64_t k0 = (int64_t)t_begin * kTileKeys;
-    int64_t k1 = k0 + (int64_t)(p.split_tiles + (split < p.split_extra ? 1 : 0)) * kTileKeys;
+    auto cw = [&](int s) -> int64_t {
+        return s < p.n_first ? (int64_t)p.w_first * s
+                             : (int64_t)p.w_first * p.n_first + (int64_t)p.w_second * (s - p.n_first);
+    };
+    const int64_t t_begin = cw(split) * p.tiles / p.cw_total;
+    const int64_t t_end = cw(split + 1) * p.tiles / p.cw_total;
+    const int64_t k0 = t_begin * kTileKeys;
+    int64_t k1 = t_end * kTileKeys;
     if (k1 > p.n_kv) k1 = p.n_kv;
     if (p.q_pos0 >= 0 && k1 > p.q_pos0 + p.n_q) k1 = p.q_pos0 + p.n_q;  // no row sees past this
     const int n_tiles = k1 > k0 ? (int)((k1 - k0 + kTileKeys - 1) / kTileKeys) : 0;
@@ -828,10 +845,19 @@ int launch_fa_decode(const FaArgs &a, hipStream_t s) {
     p.n_kv = n_kv;
     p.qscale = a.scale * kLog2e;
     p.n_splits = decode_splits(n_kv);
-    // whole 64-key tiles per split: no tile is read by two splits
-    const int64_t tiles = (n_kv + kTileKeys - 1) / kTileKeys;
-    p.split_tiles = (int)(tiles / p.n_splits);
-    p.split_extra = (int)(tiles % p.n_splits);
+    // whole 64-key tiles per split: no tile is read by two splits. With two
+    // workgroups per CU, the ones dispatched first (ids below the CU count, i.e.
+    // splits below half of it) issue ahead of the second round on the same CU
+    // (the older wavefront wins the arbitration) and run faster: they take the
+    // larger share, kFirstRoundWeight : kSecondRoundWeight, so that both rounds
+    // end together instead of the second running on alone.
+    p.tiles = (n_kv + kTileKeys - 1) / kTileKeys;
+    const int cus = device_cu_count();
+    p.n_first = 2 * p.n_splits > cus ? cus / 2 : p.n_splits;
+    if (p.n_first > p.n_splits) p.n_first = p.n_splits;
+    p.w_first = p.n_first < p.n_splits ? kFirstRoundWeight : 1;
+    p.w_second = p.n_first < p.n_splits ? kSecondRoundWeight : 1;
+    p.cw_total = (int64_t)p.w_first * p.n_first + (int64_t)p.w_second * (p.n_splits - p.n_first);
     const size_t need = fa_decode_workspace(n_q, H, n_kv);
     if (!a.ws || a.ws_bytes < need)
         return set_error(SQA_ERR_WORKSPACE, "flash_attn_ext: workspace %zu bytes < %zu needed", a.ws_bytes, need);
