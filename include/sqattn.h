@@ -34,6 +34,7 @@ extern "C" {
 #define SQA_TYPE_F32 0
 #define SQA_TYPE_F16 1
 #define SQA_TYPE_Q4_0 2
+#define SQA_TYPE_Q4_K 12
 #define SQA_TYPE_I32 26
 #define SQA_TYPE_I64 27
 
@@ -222,6 +223,32 @@ int sqa_sigmoid_mul(const sqa_tensor *dst, const sqa_tensor *x, const sqa_tensor
  * (0x0000) and masks the rest (0xFC00 = -inf); same contents as
  * fill_mask_rows (reference: src/model/graph.rs:534-576) without the host pass. */
 int sqa_fill_causal_mask(const sqa_tensor *mask, int64_t step_start, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* W_o output projection                                                     */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * dst = W . (x * sigmoid(gate)): the gate and W_o projection that end the
+ * full-attention layer (reference: ggml_sigmoid, ggml_mul and
+ * ggml_mul_mat(attn_output, gated) at src/model/attn.rs:281-285; attn_output
+ * declared at src/model/weights.rs:438).
+ *   w    Q4_K [K, N]  ggml's block_q4_K rows (K % 256 == 0, N % 16 == 0,
+ *                     16-byte aligned rows), K = n_head * head_dim, N = n_embd
+ *   x    F32  [K, M]  the attention output of M tokens (unit element stride)
+ *   gate F32  [K, M]  or NULL (then dst = W . x)
+ *   dst  F32  [N, M]  16-byte aligned rows
+ * The weights enter as exact codes and (scale, min) pairs; the gated
+ * activations as an fp16 hi + lo pair (about 22 bits, so |x| must stay below
+ * 65504); products accumulate in fp32. ggml's CPU path instead rounds the
+ * activations to 8 bits (its q8_K vec_dot type): this result is the closer of
+ * the two to the exact W . x.
+ */
+size_t sqa_out_proj_workspace_size(const sqa_tensor *w, const sqa_tensor *x);
+int sqa_supports_out_proj(const sqa_tensor *w, const sqa_tensor *x, const sqa_tensor *gate,
+                          const sqa_tensor *dst);
+int sqa_out_proj(const sqa_tensor *w, const sqa_tensor *x, const sqa_tensor *gate, const sqa_tensor *dst,
+                 void *workspace, size_t workspace_bytes, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* KV cache bookkeeping (host only: no device calls)                         */

@@ -470,6 +470,87 @@ int orc_rope_norm_f32(const sqa_tensor *dst, const sqa_tensor *src, const sqa_te
     return SQA_OK;
 }
 
+/* -------------------------------------------- W_o projection: Q4_K x F32 --- */
+
+/* Q4_K super-block (ggml block_q4_K, 256 values, 144 bytes):
+ *   bytes 0-1   d     fp16, scale of the sub-block scales
+ *   bytes 2-3   dmin  fp16, scale of the sub-block mins
+ *   bytes 4-15  12 bytes of 6-bit (scale, min) pairs for the 8 sub-blocks of 32:
+ *               sub-block s < 4: scale = b[s] & 63,           min = b[s+4] & 63
+ *               sub-block s >= 4: scale = (b[s+4] & 15) | (b[s-4] >> 6) << 4,
+ *                                 min   = (b[s+4] >> 4) | (b[s]   >> 6) << 4
+ *   bytes 16-143 codes: byte l of 32-byte group j holds value 64j + l in its
+ *               low nibble and value 64j + 32 + l in its high nibble
+ * value = (d * scale) * code - (dmin * min), each product in fp32 (both exact:
+ * 11 + 6 significant bits), one rounding at the subtraction. */
+static void q4k_scale_min(const uint8_t *b, int s, int *sc, int *mn) {
+    if (s < 4) {
+        *sc = b[s] & 63;
+        *mn = b[s + 4] & 63;
+    } else {
+        *sc = (b[s + 4] & 15) | ((b[s - 4] >> 6) << 4);
+        *mn = (b[s + 4] >> 4) | ((b[s] >> 6) << 4);
+    }
+}
+
+void orc_dequantize_row_q4_K(const uint8_t *x, float *y, int64_t k) {
+    for (int64_t i = 0; i < k / 256; ++i) {
+        const uint8_t *blk = x + 144 * i;
+        const float d = orc_fp16_to_fp32((uint16_t)(blk[0] | (blk[1] << 8)));
+        const float dmin = orc_fp16_to_fp32((uint16_t)(blk[2] | (blk[3] << 8)));
+        const uint8_t *sc = blk + 4, *qs = blk + 16;
+        for (int j = 0; j < 4; ++j) {
+            int s0, m0, s1, m1;
+            q4k_scale_min(sc, 2 * j, &s0, &m0);
+            q4k_scale_min(sc, 2 * j + 1, &s1, &m1);
+            const float dl = d * (float)s0, ml = dmin * (float)m0;
+            const float dh = d * (float)s1, mh = dmin * (float)m1;
+            float *yo = y + 256 * i + 64 * j;
+            for (int l = 0; l < 32; ++l) {
+                yo[l] = dl * (float)(qs[32 * j + l] & 15) - ml;
+                yo[32 + l] = dh * (float)(qs[32 * j + l] >> 4) - mh;
+            }
+        }
+    }
+}
+
+/* dst[N, M] = W[K, N]^T . xg[K, M] (ggml_mul_mat(W, xg) with ne = [K, N] and
+ * [K, M]), xg = x * sigmoid(gate) in fp32 as ggml_sigmoid + ggml_mul compute it
+ * (or x when gate is NULL). The weights are dequantized to fp32 as above and
+ * every row dot is accumulated in double: the exact product of what ggml's
+ * CPU path would multiply before it rounds the activations to 8 bits. */
+int orc_out_proj(const sqa_tensor *dst, const sqa_tensor *w, const sqa_tensor *x, const sqa_tensor *gate) {
+    if (!dst || !w || !x) return SQA_ERR_INVALID;
+    const int64_t K = w->ne[0], N = w->ne[1], M = x->ne[1];
+    if (w->type != SQA_TYPE_Q4_K || K % 256 || x->ne[0] != K || dst->ne[0] != N || dst->ne[1] != M)
+        return SQA_ERR_INVALID;
+    float *xg = (float *)malloc((size_t)(K * M) * sizeof(float));
+    float *wd = (float *)malloc((size_t)(K * N) * sizeof(float));
+    if (!xg || !wd) {
+        free(xg);
+        free(wd);
+        return SQA_ERR_INVALID;
+    }
+    for (int64_t t = 0; t < M; ++t) {
+        const float *xr = (const float *)((const char *)x->data + t * x->nb[1]);
+        const float *gr = gate ? (const float *)((const char *)gate->data + t * gate->nb[1]) : NULL;
+        for (int64_t k = 0; k < K; ++k) xg[t * K + k] = gr ? xr[k] * (1.f / (1.f + expf(-gr[k]))) : xr[k];
+    }
+    for (int64_t n = 0; n < N; ++n)
+        orc_dequantize_row_q4_K((const uint8_t *)w->data + n * w->nb[1], wd + n * K, K);
+#pragma omp parallel for schedule(static)
+    for (int64_t n = 0; n < N; ++n) {
+        for (int64_t t = 0; t < M; ++t) {
+            double acc = 0.0;
+            for (int64_t k = 0; k < K; ++k) acc += (double)wd[n * K + k] * (double)xg[t * K + k];
+            ((float *)((char *)dst->data + t * dst->nb[1]))[n] = (float)acc;
+        }
+    }
+    free(xg);
+    free(wd);
+    return SQA_OK;
+}
+
 int orc_max_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

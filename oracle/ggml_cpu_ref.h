@@ -33,6 +33,12 @@
  *                                          rope_ref, tests/attn_test.rs:148-208)
  *   orc_rope_norm_set_rows_q4_0          - norm -> rope -> set_rows for K, and
  *   orc_rope_norm_f32                      norm -> rope for Q (src/model/attn.rs:166-200)
+ *   orc_dequantize_row_q4_K              - ggml dequantize_row_q4_K: the Q4_K weight format
+ *                                          (the model's main quant type, tests/kernel_verify.rs:
+ *                                          553-557) of attn_output.weight (src/model/weights.rs:438)
+ *   orc_out_proj                         - ggml_mul_mat(attn_output, attn_out * sigmoid(gate)),
+ *                                          the W_o projection of src/model/attn.rs:281-285, as
+ *                                          an fp64 GEMM over the fp32 dequantized weights
  */
 #ifndef GGML_CPU_REF_H
 #define GGML_CPU_REF_H
@@ -78,6 +84,9 @@ int orc_rope_norm_set_rows_q4_0(const sqa_tensor *dst, const sqa_tensor *src, co
                                 float eps, const sqa_tensor *pos, const sqa_rope *rope, const sqa_tensor *idx);
 int orc_rope_norm_f32(const sqa_tensor *dst, const sqa_tensor *src, const sqa_tensor *norm_w, float eps,
                       const sqa_tensor *pos, const sqa_rope *rope);
+
+void orc_dequantize_row_q4_K(const uint8_t *x, float *y, int64_t k);
+int orc_out_proj(const sqa_tensor *dst, const sqa_tensor *w, const sqa_tensor *x, const sqa_tensor *gate);
 
 int orc_max_threads(void);
 

@@ -20,7 +20,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_I32, TYPE_I64 = 0, 1, 2, 26, 27
+TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q4_K, TYPE_I32, TYPE_I64 = 0, 1, 2, 12, 26, 27
 Q8_X86, Q8_SCALAR = 0, 1
 QK = 32
 Q4_BLOCK = 18
@@ -103,6 +103,8 @@ def lib():
         L.orc_rope_theta_scale.argtypes = [R]
         L.orc_rope_norm_set_rows_q4_0.argtypes = [P, P, P, ctypes.c_float, P, R, P]
         L.orc_rope_norm_f32.argtypes = [P, P, P, ctypes.c_float, P, R]
+        L.orc_dequantize_row_q4_K.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        L.orc_out_proj.argtypes = [P, P, P, P]
         L.orc_max_threads.restype = ctypes.c_int
         _lib = L
     return _lib
@@ -323,5 +325,40 @@ def rope_norm_f32(src, norm_w, eps, pos, rope):
     to = tensor(TYPE_F32, [D, n_head, n_tok], [4, D * 4, n_head * D * 4], out)
     rc = lib().orc_rope_norm_f32(ctypes.byref(to), ctypes.byref(ts), ctypes.byref(tw) if tw is not None else None,
                                  eps, ctypes.byref(tp), ctypes.byref(rope))
+    assert rc == 0, rc
+    return out
+
+
+Q4K_BLOCK = 144  # bytes per 256-value Q4_K super-block
+
+
+def dequantize_q4_K(wq, k):
+    """Rows of Q4_K bytes (n, k // 256 * 144) -> float32 (n, k), ggml's dequantize_row_q4_K."""
+    wq = np.ascontiguousarray(wq, dtype=np.uint8).reshape(-1, k // 256 * Q4K_BLOCK)
+    out = np.empty((wq.shape[0], k), np.float32)
+    for i in range(wq.shape[0]):
+        lib().orc_dequantize_row_q4_K(_ptr(wq[i]), _ptr(out[i]), k)
+    return out
+
+
+def out_proj(wq, x, gate=None):
+    """W_o projection (src/model/attn.rs:281-285): wq Q4_K rows (N, K // 256 * 144),
+    x (M, K) float32 attention output, gate (M, K) or None -> (M, N) float32 =
+    (x * sigmoid(gate)) @ dequant(W)^T accumulated in double."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    wq = np.ascontiguousarray(wq, dtype=np.uint8).reshape(-1, K // 256 * Q4K_BLOCK)
+    N = wq.shape[0]
+    out = np.empty((M, N), np.float32)
+    tw = tensor(TYPE_Q4_K, [K, N], [Q4K_BLOCK, K // 256 * Q4K_BLOCK], wq)
+    tx = tensor(TYPE_F32, [K, M], [4, K * 4], x)
+    to = tensor(TYPE_F32, [N, M], [4, N * 4], out)
+    tg = None
+    if gate is not None:
+        gate = np.ascontiguousarray(gate, dtype=np.float32)
+        assert gate.shape == x.shape
+        tg = tensor(TYPE_F32, [K, M], [4, K * 4], gate)
+    rc = lib().orc_out_proj(ctypes.byref(to), ctypes.byref(tw), ctypes.byref(tx),
+                            ctypes.byref(tg) if tg is not None else None)
     assert rc == 0, rc
     return out

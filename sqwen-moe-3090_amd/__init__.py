@@ -20,14 +20,15 @@ import torch
 __all__ = [
     "Tensor", "lib", "last_error", "SqaError", "set_rows_q4_0", "flash_attn_ext",
     "flash_attn_ext_causal", "flash_attn_ext_static", "sigmoid_mul", "fill_causal_mask", "supports_flash_attn_ext",
-    "flash_attn_workspace_size", "KvCache", "cache_view", "row_bytes", "profile_begin", "profile_end",
+    "flash_attn_workspace_size", "out_proj", "out_proj_workspace_size", "KvCache", "cache_view", "row_bytes", "profile_begin", "profile_end",
     "profile_get", "Rope", "rope_params", "rope_norm_set_rows_q4_0", "rope_norm_f32",
 ]
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libsqattn.so")
 
-TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_I32, TYPE_I64 = 0, 1, 2, 26, 27
+TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q4_K, TYPE_I32, TYPE_I64 = 0, 1, 2, 12, 26, 27
+Q4_K_BLOCK = 144  # bytes per 256-value Q4_K super-block
 QK4_0 = 32
 Q4_0_BLOCK = 18
 KV_PAD = 256
@@ -117,6 +118,9 @@ def lib():
             "sqa_flash_attn_ext_causal": (ctypes.c_int, [P, P, P, i64, P, f32, P, vp, sz, vp]),
             "sqa_flash_attn_ext_static": (ctypes.c_int, [P, P, P, P, f32, f32, f32, P, vp]),
             "sqa_sigmoid_mul": (ctypes.c_int, [P, P, P, vp]),
+            "sqa_out_proj_workspace_size": (sz, [P, P]),
+            "sqa_supports_out_proj": (ctypes.c_int, [P, P, P, P]),
+            "sqa_out_proj": (ctypes.c_int, [P, P, P, P, vp, sz, vp]),
             "sqa_fill_causal_mask": (ctypes.c_int, [P, i64, vp]),
             "sqa_kv_cache_layer_bytes": (sz, [i64, i64, i64]),
             "sqa_kv_cache_create": (vp, [i32, i64, i64, i64, ctypes.POINTER(vp), ctypes.POINTER(vp)]),
@@ -343,6 +347,38 @@ def sigmoid_mul(x, gate, out=None, stream=None):
     n1, n0 = x.shape
     d = [Tensor.make(TYPE_F32, [n0, n1], [4, t.stride(0) * 4], t.data_ptr()) for t in (out, x, gate)]
     _check(lib().sqa_sigmoid_mul(ctypes.byref(d[0]), ctypes.byref(d[1]), ctypes.byref(d[2]), _stream(stream)))
+    return out
+
+
+def _out_proj_descs(w, x, gate, out):
+    """w: uint8 (N, K // 256 * 144) Q4_K rows; x, gate: float32 (M, K); out: float32 (M, N)."""
+    M, K = x.shape
+    N = w.shape[0]
+    tw = Tensor.make(TYPE_Q4_K, [K, N], [Q4_K_BLOCK, w.stride(0)], w.data_ptr())
+    tx = Tensor.make(TYPE_F32, [K, M], [4, x.stride(0) * 4], x.data_ptr())
+    tg = None if gate is None else Tensor.make(TYPE_F32, [K, M], [4, gate.stride(0) * 4], gate.data_ptr())
+    to = None if out is None else Tensor.make(TYPE_F32, [N, M], [4, out.stride(0) * 4], out.data_ptr())
+    return tw, tx, tg, to
+
+
+def out_proj_workspace_size(w, x):
+    tw, tx, _, _ = _out_proj_descs(w, x, None, None)
+    return int(lib().sqa_out_proj_workspace_size(ctypes.byref(tw), ctypes.byref(tx)))
+
+
+def out_proj(w, x, gate=None, out=None, workspace=None, stream=None):
+    """W_o projection (attn.rs:281-285): out (M, N) = (x * sigmoid(gate)) @ W^T with
+    W the Q4_K weight rows w (N, K // 256 * 144) and x, gate (M, K) float32."""
+    M, K = x.shape
+    if out is None:
+        out = torch.empty((M, w.shape[0]), dtype=torch.float32, device=x.device)
+    tw, tx, tg, to = _out_proj_descs(w, x, gate, out)
+    need = int(lib().sqa_out_proj_workspace_size(ctypes.byref(tw), ctypes.byref(tx)))
+    if workspace is None:
+        workspace, _ = _workspace(need, x.device)
+    _check(lib().sqa_out_proj(ctypes.byref(tw), ctypes.byref(tx), _ref(tg), ctypes.byref(to),
+                              workspace.data_ptr() if workspace is not None else None,
+                              workspace.numel() if workspace is not None else 0, _stream(stream)))
     return out
 
 

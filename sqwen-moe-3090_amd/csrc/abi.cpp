@@ -363,6 +363,52 @@ int sqa_sigmoid_mul(const sqa_tensor *dst, const sqa_tensor *x, const sqa_tensor
     return launch_sigmoid_mul(*dst, *x, *gate, (hipStream_t)stream);
 }
 
+static int check_out_proj(const sqa_tensor *w, const sqa_tensor *x, const sqa_tensor *gate,
+                          const sqa_tensor *dst) {
+    if (!w || !x) return set_error(SQA_ERR_INVALID, "out_proj: null tensor");
+    const int64_t K = w->ne[0], N = w->ne[1], M = x->ne[1];
+    if (w->type != SQA_TYPE_Q4_K || w->ne[2] != 1 || w->ne[3] != 1)
+        return set_error(SQA_ERR_UNSUPPORTED, "out_proj: weight must be a 2-D Q4_K tensor");
+    if (K <= 0 || K % 256 || N % 16)
+        return set_error(SQA_ERR_UNSUPPORTED, "out_proj: need K %% 256 == 0 and N %% 16 == 0 (K=%lld, N=%lld)",
+                         (long long)K, (long long)N);
+    if (w->nb[1] % 16 || (uintptr_t)w->data % 16)
+        return set_error(SQA_ERR_UNSUPPORTED, "out_proj: weight rows must be 16-byte aligned");
+    if (x->type != SQA_TYPE_F32 || x->nb[0] != 4 || x->nb[1] % 4 || x->ne[0] != K || x->ne[2] != 1 || x->ne[3] != 1)
+        return set_error(SQA_ERR_INVALID, "out_proj: x must be F32 [K, M] with unit element stride");
+    if (gate && (gate->type != SQA_TYPE_F32 || gate->nb[0] != 4 || gate->nb[1] % 4 || gate->ne[0] != K ||
+                 gate->ne[1] != M || gate->ne[2] != 1 || gate->ne[3] != 1))
+        return set_error(SQA_ERR_INVALID, "out_proj: gate must be F32 [K, M] with unit element stride");
+    if (dst) {
+        if (dst->type != SQA_TYPE_F32 || dst->nb[0] != 4 || dst->ne[0] != N || dst->ne[1] != M ||
+            dst->ne[2] != 1 || dst->ne[3] != 1)
+            return set_error(SQA_ERR_INVALID, "out_proj: dst must be F32 [N, M]");
+        if (dst->nb[1] % 16 || (uintptr_t)dst->data % 16)
+            return set_error(SQA_ERR_UNSUPPORTED, "out_proj: dst rows must be 16-byte aligned");
+    }
+    if (M > 0 && N > 0 && (!w->data || !x->data || (gate && !gate->data) || (dst && !dst->data)))
+        return set_error(SQA_ERR_INVALID, "out_proj: null data pointer");
+    return SQA_OK;
+}
+
+size_t sqa_out_proj_workspace_size(const sqa_tensor *w, const sqa_tensor *x) {
+    if (!w || !x) return 0;
+    return out_proj_workspace(w->ne[0], x->ne[1]);
+}
+
+int sqa_supports_out_proj(const sqa_tensor *w, const sqa_tensor *x, const sqa_tensor *gate,
+                          const sqa_tensor *dst) {
+    return check_out_proj(w, x, gate, dst) == SQA_OK ? 1 : 0;
+}
+
+int sqa_out_proj(const sqa_tensor *w, const sqa_tensor *x, const sqa_tensor *gate, const sqa_tensor *dst,
+                 void *workspace, size_t workspace_bytes, void *stream) {
+    if (!dst) return set_error(SQA_ERR_INVALID, "out_proj: null dst");
+    const int rc = check_out_proj(w, x, gate, dst);
+    if (rc != SQA_OK) return rc;
+    return launch_out_proj(*w, *x, gate, *dst, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
 int sqa_fill_causal_mask(const sqa_tensor *mask, int64_t step_start, void *stream) {
     if (!mask || (mask->ne[0] * mask->ne[1] > 0 && !mask->data))
         return set_error(SQA_ERR_INVALID, "fill_causal_mask: null tensor");

@@ -57,6 +57,10 @@ constexpr int kMaxSplits = 256;
 int launch_fa_combine(const float *part_acc, const float *part_ml, int n_splits, int rows_total,
                       float *dst, const sqa_tensor *gate, int H, hipStream_t s);
 int launch_fa_decode(const FaArgs &a, hipStream_t s);
+// W_o projection dst[N, M] = W[K, N] (Q4_K) . (x * sigmoid(gate)) (gate may be null)
+size_t out_proj_workspace(int64_t K, int64_t M);
+int launch_out_proj(const sqa_tensor &w, const sqa_tensor &x, const sqa_tensor *gate, const sqa_tensor &dst,
+                    void *ws, size_t ws_bytes, hipStream_t s);
 size_t fa_prefill_workspace(int64_t n_q, int64_t H, int64_t Hkv, int64_t n_kv);
 int launch_fa_prefill(const FaArgs &a, hipStream_t s);
 
