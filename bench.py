@@ -293,6 +293,47 @@ def producer_leg(sqa, torch, dev, steps, warmup):
     return out
 
 
+def out_proj_leg(sqa, torch, dev, np, steps, warmup):
+    """W_o projection per layer (attn.rs:281-285): dst = W . (x * sigmoid(gate)) with
+    W a Q4_K [4096, 2048] weight (n_head 16 x head_dim 256 in, n_embd 2048 out) of
+    random codes and scales, for a decode token, a 2-token verify and the 512-token
+    ubatch. Decode is bound by the weight bytes; the ubatch by the MFMA work."""
+    K, N = H * D, 2048
+    rng = np.random.default_rng(7)
+    out = {}
+    ws_w = []
+    for _ in range(N_LAYERS):
+        w = rng.integers(0, 256, (N, K // 256, 144), dtype=np.uint8)
+        w[:, :, 0:2] = rng.uniform(2e-4, 4e-3, (N, K // 256)).astype(np.float16).view(np.uint8).reshape(N, -1, 2)
+        w[:, :, 2:4] = rng.uniform(0, 4e-3, (N, K // 256)).astype(np.float16).view(np.uint8).reshape(N, -1, 2)
+        ws_w.append(torch.from_numpy(w.reshape(N, -1)).to(dev))
+    w_bytes = N * K // 256 * 144
+    for M in (1, 2, PP_N_Q):
+        x = torch.randn((M, K), device=dev)
+        g = torch.randn((M, K), device=dev)
+        o = torch.empty((M, N), device=dev)
+        need = sqa.out_proj_workspace_size(ws_w[0], x)
+        wsp = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+
+        def step():
+            for w in ws_w:
+                sqa.out_proj(w, x, g, out=o, workspace=wsp)
+
+        for _ in range(warmup):
+            step()
+        ms = time_steps(torch, step, steps) / steps
+        sqa.profile_begin(steps * N_LAYERS + 8)
+        time_steps(torch, step, steps)
+        sqa.profile_end()
+        tt, c = sqa.profile_get("out_proj")
+        us = tt / c * 1e3
+        out[f"m{M}"] = {"per_layer_us": round(ms * 1e3 / N_LAYERS, 2), "kernels_us": round(us, 2),
+                        "weight_GB/s": round(w_bytes / (us * 1e-6) / 1e9, 1),
+                        "TFLOP/s": round(2 * N * K * M / (us * 1e-6) / 1e12, 2)}
+    out["shape"] = {"K": K, "N": N, "weight": "Q4_K", "weight_bytes": w_bytes}
+    return out
+
+
 def host_cpu():
     """(CPU model, logical CPUs usable by this process)."""
     model = "unknown"
@@ -376,6 +417,7 @@ def main():
     ap.add_argument("--no-stack", action="store_true", help="skip the 10-layer ubatch-2048 stack leg")
     ap.add_argument("--no-producer", action="store_true", help="skip the K/Q producer (norm + rope) leg")
     ap.add_argument("--no-graph", action="store_true", help="skip the graph-replay decode timing")
+    ap.add_argument("--no-out-proj", action="store_true", help="skip the W_o projection leg")
     ap.add_argument("--copy-ref", action="store_true",
                     help="run a plain 256 MiB device copy at the end (counter calibration)")
     args = ap.parse_args()
@@ -476,6 +518,9 @@ def main():
         torch.cuda.empty_cache()
     if not args.no_producer:
         result["producer_rope_norm"] = producer_leg(sqa, torch, dev, max(2, args.steps // 2), 2)
+        torch.cuda.empty_cache()
+    if not args.no_out_proj:
+        result["out_proj_wo"] = out_proj_leg(sqa, torch, dev, np, max(2, args.steps // 2), 2)
         torch.cuda.empty_cache()
 
     if not args.no_cpu:
