@@ -31,11 +31,13 @@
 //     factors go to LDS.
 //   value wave 4 + w, the same 32 rows, holds their O (128 registers) one tile
 //     behind: O = alpha O + P V per block b (alpha only when a maximum moved)
-//     with A = P d_v 2^e as an fp16 hi + lo pair built by packed fp16 ops (two
+//     with A = P d_v as an fp16 hi + lo pair built by packed fp16 ops (two
 //     MFMAs, ~22 bits) and B = the exact V codes, so every product is exact in
-//     fp32. 2^e is one power of two per KV head that brings max |d_v| into
-//     [1, 2): it keeps A clear of fp16 subnormals and overflow, and l is scaled
-//     by the same factor.
+//     fp32. P carries 2^ep, one power of two per KV head (the largest |d_v| of
+//     the head brought toward [1, 2), ep clamped to [-6, 7] so that P stays
+//     finite): it keeps A clear of fp16 subnormals and overflow for every
+//     |d_v| < 16376, and l, summed from the same P, carries the same factor.
+//     The d_v and V operands of a tile are read ahead of the MFMAs that use them.
 //   A masked key contributes exactly 0 even over NaN/Inf block scales (as ggml's
 //   CPU loop, which skips it): a -inf mask entry replaces the logit, and the
 //   pre-pass reads NaN/Inf V scales as 0.
@@ -425,8 +427,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
     };
     if (n_tiles > 0) issue(0, -1);
 
-    // e with max |d_v| * 2^e in [1, 2) (at most 2^15, the largest power of two in
-    // fp16): the value waves scale d_v by 2^e, l carries the same factor
+    // e2 with max |d_v| * 2^e2 in [1, 2) (at most 15)
     int e2 = 0;
     {
         const float dm = h2f(p.dvmax[kvh]);
@@ -436,6 +437,11 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             e2 = 1 - e < 15 ? 1 - e : 15;
         }
     }
+    // 2^ep with ep = e2 clamped to [-6, 7] rides on P (the score waves' exp2
+    // argument): P 2^ep <= 2^(kSlack + 7) stays finite in fp16 and A = P 2^ep d_v
+    // below 2^9 for max |d_v| in [2^-8, 2^7), below 65504 for every |d_v| < 16376.
+    // O and l both carry it, so it cancels in O / l.
+    const int ep = e2 < -6 ? -6 : (e2 > 7 ? 7 : e2);
     const int nh = (n >> 3) & 1;
 
     // The two kinds of wave run separate code with the same barrier count:
@@ -582,7 +588,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                     l_part[rg] *= alpha;
                     m_run[rg] = m_new;
                 }
-                const float mref = m_run[rg] == -INFINITY ? 0.0f : m_run[rg];
+                const float mref = (m_run[rg] == -INFINITY ? 0.0f : m_run[rg]) - (float)ep;
                 float pf[8], psum = 0.0f;
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj) {
@@ -627,9 +633,6 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
     const int v_off0 = 64 * n + 16 * (g ^ ((n >> 1) & 3)) + 8 * nh;
     const int v_off1 = v_off0 ^ 8;
     const int p_off = w * (kRG * 2048) + 16 * lane;
-    const _Float16 d2e_s = (_Float16)ldexpf(1.0f, e2);
-    const half8 d2e = {d2e_s, d2e_s, d2e_s, d2e_s, d2e_s, d2e_s, d2e_s, d2e_s};
-    const float l_scale = ldexpf(1.0f, e2);  // O carries 2^e: l gets it too
     floatx4 acc[kRG][16];
 #pragma unroll
     for (int rg = 0; rg < kRG; ++rg)
@@ -664,35 +667,47 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                 for (int T = 0; T < 16; ++T) acc[rg][T] *= a4;
             }
         }
+        // d_v of the 8 blocks and V of block 0 first, then V of block b + 1 while
+        // block b computes: the LDS latency stays off the MFMA chain
+        uint4 dvr[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) dvr[b] = *reinterpret_cast<const uint4 *>(vs + kOffDv + 64 * b + 16 * g);
+        half8 bvn[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) bvn[hf] = lds_half8(smem, vb0 + 1024 * hf, vb1 + 1024 * hf);
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
-            half8 dvb;
-            {
-                const uint4 u = *reinterpret_cast<const uint4 *>(vs + kOffDv + 64 * b + 16 * g);
-                __builtin_memcpy(&dvb, &u, 16);
-            }
-            dvb *= d2e;  // d_v 2^e, exact (a power of two, |d_v| 2^e < 2)
-            // A = P 2^e d_v as an fp16 hi + lo pair (22 bits): the products with the
-            // exact V codes are then exact in fp32, so a row that a few keys
-            // dominate carries no fp16 rounding of P d_v into its output.
-            half8 bv[2];
+            const half8 bv[2] = {bvn[0], bvn[1]};
+            if (b < 7) {
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf) bv[hf] = lds_half8(smem, vb0 + 1024 * (2 * b + hf), vb1 + 1024 * (2 * b + hf));
+                for (int hf = 0; hf < 2; ++hf)
+                    bvn[hf] = lds_half8(smem, vb0 + 1024 * (2 * b + 2 + hf), vb1 + 1024 * (2 * b + 2 + hf));
+            }
+            half8 dvb;
+            __builtin_memcpy(&dvb, &dvr[b], 16);
+            // A = P 2^ep d_v as an fp16 hi + lo pair (22 bits): the products with the
+            // exact V codes are then exact in fp32, so a row that a few keys
+            // dominate carries no fp16 rounding of P d_v into its output. Ph d_v has
+            // at most 22 significant bits, so its residual after rounding to fp16
+            // (at most 11 bits) is exact in one fma; Pl d_v is 2^-11 of it and
+            // rounds once.
+            half8 ah[kRG], al[kRG];
 #pragma unroll
             for (int rg = 0; rg < kRG; ++rg) {
-                // A = P d_v 2^e as hi + lo in packed fp16: Ph d_v has at most 22
-                // significant bits, so its residual after rounding to fp16 (at most
-                // 11 bits) is exact in one fma; Pl d_v is 2^-11 of it and rounds once
-                const half8 a = ph[rg] * dvb;
-                const half8 r = __builtin_elementwise_fma(ph[rg], dvb, -a);
-                const half8 al = __builtin_elementwise_fma(pl[rg], dvb, r);
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-                    const int T = 2 * b + hf;
-                    acc[rg][T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bv[hf], acc[rg][T], 0, 0, 0);
-                    acc[rg][T] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv[hf], acc[rg][T], 0, 0, 0);
-                }
+                ah[rg] = ph[rg] * dvb;
+                const half8 r = __builtin_elementwise_fma(ph[rg], dvb, -ah[rg]);
+                al[rg] = __builtin_elementwise_fma(pl[rg], dvb, r);
             }
+#pragma unroll
+            for (int rg = 0; rg < kRG; ++rg)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+                    acc[rg][2 * b + hf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[rg], bv[hf], acc[rg][2 * b + hf], 0, 0, 0);
+#pragma unroll
+            for (int rg = 0; rg < kRG; ++rg)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+                    acc[rg][2 * b + hf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[rg], bv[hf], acc[rg][2 * b + hf], 0, 0, 0);
         }
     }
     __syncthreads();  // m and l of the rows ...
@@ -706,7 +721,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             const int qrow = q_base + r / p.G, hrow = kvh * p.G + r % p.G;
             if (qrow >= p.n_q) continue;
             const float mrow = n_tiles > 0 ? ml[rg * 32 + 2 * (4 * g + i)] : -INFINITY;
-            const float lrow = n_tiles > 0 ? ml[rg * 32 + 2 * (4 * g + i) + 1] * l_scale : 0.0f;
+            const float lrow = n_tiles > 0 ? ml[rg * 32 + 2 * (4 * g + i) + 1] : 0.0f;
             const int64_t ridx = (int64_t)qrow * p.H + hrow;
             if (p.n_splits == 1) {
                 const float inv = lrow == 0.0f ? 0.0f : 1.0f / lrow;
@@ -726,7 +741,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                 for (int T = 0; T < 16; ++T) pa_out[16 * T + n] = acc[rg][T][i];
                 if (n == 0) {
                     // the combine works in base e: m * ln 2 (acc and l of every split
-                    // carry the same 2^e, which cancels in the merge)
+                    // carry the same 2^ep, which cancels in the merge)
                     p.part_ml[((int64_t)split * rows_total + ridx) * 2] =
                         mrow == -INFINITY ? mrow : mrow * 0.6931471805599453f;
                     p.part_ml[((int64_t)split * rows_total + ridx) * 2 + 1] = lrow;

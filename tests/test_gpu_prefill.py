@@ -106,6 +106,22 @@ def test_chunk_at_context_start_with_outliers(sqa, orc, dev, n_q, n_kv, start):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("scale_v", [1e-4, 3e-2, 500.0, 2000.0])
+def test_prefill_v_scale_range(sqa, orc, dev, scale_v):
+    """V of any size the kernel admits (|d_v| < 16376): the softmax weights carry
+    2^ep, ep from the largest |d_v| of the head clamped to [-6, 7], so that P d_v
+    keeps 22 bits without overflow; 1e-4 and 500 reach the two ends of the clamp,
+    2000 (|d_v| about 5000 on the outlier channels) nears the overflow bound."""
+    q, kq, vq = qkv(orc, 77, 300, 512, outliers=5, scale_v=scale_v)
+    mask = orc.causal_mask(300, 512, 212)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    err = rel_err(got, ref)
+    dv = np.abs(vq.reshape(-1, 18)[:, :2].copy().view(np.float16)).max()
+    print(f"prefill V x{scale_v} (max |d_v| {dv:.3g}): max err / rms = {err:.3e}")
+    assert err <= TOL
+
+
 def test_prefill_masked_rows_with_garbage_bytes(sqa, orc, dev):
     """Masked cache rows holding 0xFF bytes (NaN block scales, what an unzeroed
     buffer may hold) or stale rows of other data (a rewound draft) do not change
