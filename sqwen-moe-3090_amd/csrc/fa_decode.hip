@@ -51,14 +51,16 @@
 //     workgroup reads the four maxima used, takes their maximum, and rescales
 //     its share (l, O, and the P values of that tile) onto it.
 //   * PV: v_mfma_f32_16x16x32_f16 with fp32 accumulation, d_v on the A side:
-//     A = P d_v of the block as an exact fp16 hi + lo pair (P arrives as an fp16
-//     hi + lo pair, ~22 bits), B = the raw nibbles as fp16 subnormals (nib *
-//     2^-24, or nib * 2^-20 for the high nibble, one v_and per two keys), and
+//     A = P d_v 2^E of the block as an exact fp16 hi + lo pair (P arrives as an
+//     fp16 hi + lo pair, ~22 bits), B = the raw nibbles as fp16 subnormals (nib
+//     * 2^-24, or nib * 2^-20 for the high nibble, one v_and per two keys), and
 //     the -8 offset as -8 * sum A from one more MFMA against ones. Every product
 //     is exact in fp32, so a row that a few keys dominate carries no fp16
 //     rounding of V or P into its output (ggml's CPU path dequantizes V to fp32
-//     exactly). P is kept at 2^-4 of its value (<= 16), so A stays finite for
-//     every |d_v| < 4094, i.e. V values up to 32752 in magnitude.
+//     exactly). P is kept at 2^-4 of its value (<= 16); 2^E is one power of
+//     two per value wavefront that puts the largest |d_v| it has seen near 2^8
+//     (lowered, with O rescaled, when a larger one comes), so A stays finite
+//     and clear of fp16 subnormals for V of any size.
 //   * A key that no row of the call sees (masked in every row, past the split
 //     or past the cache end) contributes exactly 0 whatever its bytes, as in
 //     ggml's CPU loop, which skips masked keys: a -inf mask entry replaces the
@@ -112,8 +114,11 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kSlack = 8.0f;  // log2 of the largest P the lazy rescale admits
 // P is stored as P 2^-kPShift (<= 2^(kSlack - kPShift) = 16) and l summed from the
-// same values, so A = P d_v stays below 65504 for every |d_v| < 4094.
+// same values; with |d_v 2^E| < 2^11, A = P d_v 2^E stays below 2^15.
 constexpr float kPShift = 4.0f;
+// Largest d_v exponent E of the value wavefronts (d_v enters A as d_v 2^E): V
+// scales below 2^-20 lose low bits of A; 2^E stays two fp16 powers of two.
+constexpr int kMaxDvExp = 28;
 // Tile shares of a first-round and a second-round split when two workgroups
 // share each CU (see launch_fa_decode).
 constexpr int kFirstRoundWeight = 2;
@@ -625,6 +630,26 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
 #pragma unroll
         for (int T = 0; T < 4; ++T) acc[T] = floatx4{0.f, 0.f, 0.f, 0.f};
         cor[0] = cor[1] = floatx4{0.f, 0.f, 0.f, 0.f};
+        // d_v enters A as d_v 2^E (E per wavefront, only ever lowered): P 2^-4 <= 16
+        // times |d_v 2^E| < 2^11 keeps A below 2^15, and the largest d_v near 2^8
+        // keeps A clear of fp16 subnormals, whatever the size of V. The partial O
+        // is scaled back by 2^-E; l does not carry E.
+        int e_dv = kMaxDvExp;
+        uint32_t dv_thr = 0;  // fp16 magnitude bits of 2^(11 - E)
+        half2v dv_s1, dv_s2;  // 2^floor(E/2), 2^(E - floor(E/2))
+        auto set_dv_scale = [&](int e) {
+            e_dv = e;
+            const int x = 11 - e;
+            dv_thr = x >= 16 ? 0x7C00u : (x >= -14 ? (uint32_t)(x + 15) << 10 : 1u << (x + 24));
+            const int e1 = e >> 1, e2 = e - e1;
+            const uint16_t b1 = (uint16_t)((e1 + 15) << 10), b2 = (uint16_t)((e2 + 15) << 10);
+            _Float16 h1, h2;
+            __builtin_memcpy(&h1, &b1, 2);
+            __builtin_memcpy(&h2, &b2, 2);
+            dv_s1 = half2v{h1, h1};
+            dv_s2 = half2v{h2, h2};
+        };
+        set_dv_scale(kMaxDvExp);
         float m_acc[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // reference max of rows 4g+i
 
         for (int tt = 0; tt <= n_tiles; ++tt) {
@@ -653,7 +678,32 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                                        ((uint64_t)((fl.z >> 16) | (fl.w & 0xFFFF0000u)) << 32);
                 da = (alive >> ckey) & 1 ? da : 0u;
                 db = (alive >> (ckey + 1)) & 1 ? db : 0u;
-                *reinterpret_cast<uint32_t *>(dv_comp + cdst) = da | (db << 16);
+                // a d_v at or above 2^(11 - E) lowers E so that the largest |d_v| of
+                // the tile lands in [2^8, 2^9); O is rescaled by the exact power of two
+                const uint32_t mag = max(da & 0x7FFFu, db & 0x7FFFu);
+                if (__any(mag >= dv_thr)) {
+                    uint32_t mx = mag;
+#pragma unroll
+                    for (int o = 32; o >= 1; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
+                    mx = (uint32_t)__builtin_amdgcn_readfirstlane((int)mx);
+                    const int ex = (int)(mx >> 10);
+                    const int lg = ex ? ex - 15 : (31 - __clz((int)mx)) - 24;  // floor(log2 max |d_v|)
+                    const int e_new = 8 - lg;
+                    if (e_new < e_dv) {
+                        const float f = __builtin_amdgcn_ldexpf(1.0f, e_new - e_dv);
+#pragma unroll
+                        for (int T = 0; T < 4; ++T) acc[T] *= f;
+                        cor[0] *= f;
+                        cor[1] *= f;
+                        set_dv_scale(e_new);
+                    }
+                }
+                uint32_t w = da | (db << 16);
+                half2v wh;
+                __builtin_memcpy(&wh, &w, 4);
+                wh = wh * dv_s1 * dv_s2;  // d_v 2^E in two exact steps (2^E may exceed fp16)
+                __builtin_memcpy(&w, &wh, 4);
+                *reinterpret_cast<uint32_t *>(dv_comp + cdst) = w;
             }
 
             // -- P rows (k-slot order) and a possible move of the reference max ---
@@ -748,6 +798,7 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
 
         // ---------------- this split's partial O (un-normalised) -----------------
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // pairs the statistics barrier
+        const float o_scale = __builtin_amdgcn_ldexpf(1.0f, -e_dv);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 4 * g + i;
@@ -756,8 +807,8 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                 float *dst = p.part_acc + ((int64_t)split * rows_total + (int64_t)tq * p.H + hq) * 256 + 64 * dq + n;
 #pragma unroll
                 for (int bl = 0; bl < 2; ++bl) {
-                    dst[32 * bl] = fmaf(acc[2 * bl][i], 16777216.0f, -8.0f * cor[bl][i]);
-                    dst[32 * bl + 16] = fmaf(acc[2 * bl + 1][i], 1048576.0f, -8.0f * cor[bl][i]);
+                    dst[32 * bl] = fmaf(acc[2 * bl][i], 16777216.0f, -8.0f * cor[bl][i]) * o_scale;
+                    dst[32 * bl + 16] = fmaf(acc[2 * bl + 1][i], 1048576.0f, -8.0f * cor[bl][i]) * o_scale;
                 }
             }
         }
