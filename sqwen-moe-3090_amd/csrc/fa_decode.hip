@@ -161,6 +161,20 @@ typedef const __attribute__((address_space(3))) uint32_t lds_u32;  // LDS dword 
 __device__ __forceinline__ uint32_t lds32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
 __device__ __forceinline__ uint32_t lds16(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
 
+// Largest of a non-negative value over the 64 lanes, in a scalar register: DPP
+// row shifts fold each row of 16 into its last lane, row broadcasts fold rows
+// into lane 63 (lanes without a source keep their own value).
+__device__ __forceinline__ int wave_max_u16(uint32_t v) {
+    int x = (int)v;
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x111, 0xf, 0xf, false));  // row_shr:1
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x112, 0xf, 0xf, false));  // row_shr:2
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x114, 0xf, 0xf, false));  // row_shr:4
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x118, 0xf, 0xf, false));  // row_shr:8
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x142, 0xa, 0xf, false));  // row_bcast:15
+    x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x143, 0xc, 0xf, false));  // row_bcast:31
+    return __builtin_amdgcn_readlane(x, 63);
+}
+
 __device__ __forceinline__ float exp2_or_zero(float a, float b) {  // 2^(a-b), 0 when a = -inf
     return a == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(a - b);
 }
@@ -667,6 +681,15 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             // 16 keys that some row of the call can see (P != 0)
             const uint4 fl = *reinterpret_cast<const uint4 *>(fbuf + pb * 4);
 
+            // -- P rows (k-slot order), read first: their latency runs under the
+            // d_v compaction below
+            const _Float16 *prow = pbuf + (pb * 16 + ra) * kPRow + 8 * g;
+            half8 pa[2], pl[2];  // P hi and lo of tile halves 0, 1
+            pa[0] = *reinterpret_cast<const half8 *>(prow);
+            pa[1] = *reinterpret_cast<const half8 *>(prow + 32);
+            pl[0] = *reinterpret_cast<const half8 *>(prow + 64);
+            pl[1] = *reinterpret_cast<const half8 *>(prow + 96);
+
             // -- d_v of the slice's two blocks for all 64 keys, in B k-slot order --
             // A key no row sees (masked, past the range or past the cache end) gets
             // d_v = 0, so its bytes, whatever they hold, add exactly 0 as ggml's CPU
@@ -678,16 +701,23 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                                        ((uint64_t)((fl.z >> 16) | (fl.w & 0xFFFF0000u)) << 32);
                 da = (alive >> ckey) & 1 ? da : 0u;
                 db = (alive >> (ckey + 1)) & 1 ? db : 0u;
+                auto store_scaled = [&]() {  // d_v 2^E in two exact steps (2^E may exceed fp16)
+                    uint32_t w = da | (db << 16);
+                    half2v wh;
+                    __builtin_memcpy(&wh, &w, 4);
+                    wh = wh * dv_s1 * dv_s2;
+                    __builtin_memcpy(&w, &wh, 4);
+                    *reinterpret_cast<uint32_t *>(dv_comp + cdst) = w;
+                };
+                store_scaled();
                 // a d_v at or above 2^(11 - E) lowers E so that the largest |d_v| of
-                // the tile lands in [2^8, 2^9); O is rescaled by the exact power of two
+                // the tile lands in [2^8, 2^9); O is rescaled by the exact power of
+                // two and the tile's d_v are stored again
                 const uint32_t mag = max(da & 0x7FFFu, db & 0x7FFFu);
                 if (__any(mag >= dv_thr)) {
-                    uint32_t mx = mag;
-#pragma unroll
-                    for (int o = 32; o >= 1; o >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
-                    mx = (uint32_t)__builtin_amdgcn_readfirstlane((int)mx);
-                    const int ex = (int)(mx >> 10);
-                    const int lg = ex ? ex - 15 : (31 - __clz((int)mx)) - 24;  // floor(log2 max |d_v|)
+                    const int mx = wave_max_u16(mag);
+                    const int ex = mx >> 10;
+                    const int lg = ex ? ex - 15 : (31 - __clz(mx)) - 24;  // floor(log2 max |d_v|)
                     const int e_new = 8 - lg;
                     if (e_new < e_dv) {
                         const float f = __builtin_amdgcn_ldexpf(1.0f, e_new - e_dv);
@@ -696,23 +726,12 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                         cor[0] *= f;
                         cor[1] *= f;
                         set_dv_scale(e_new);
+                        store_scaled();
                     }
                 }
-                uint32_t w = da | (db << 16);
-                half2v wh;
-                __builtin_memcpy(&wh, &w, 4);
-                wh = wh * dv_s1 * dv_s2;  // d_v 2^E in two exact steps (2^E may exceed fp16)
-                __builtin_memcpy(&w, &wh, 4);
-                *reinterpret_cast<uint32_t *>(dv_comp + cdst) = w;
             }
 
-            // -- P rows (k-slot order) and a possible move of the reference max ---
-            const _Float16 *prow = pbuf + (pb * 16 + ra) * kPRow + 8 * g;
-            half8 pa[2], pl[2];  // P hi and lo of tile halves 0, 1
-            pa[0] = *reinterpret_cast<const half8 *>(prow);
-            pa[1] = *reinterpret_cast<const half8 *>(prow + 32);
-            pl[0] = *reinterpret_cast<const half8 *>(prow + 64);
-            pl[1] = *reinterpret_cast<const half8 *>(prow + 96);
+            // -- a possible move of the reference max ---------------------------------
             if ((fl.x | fl.y | fl.z | fl.w) & 1u) {
                 const float *mr = mbuf + pb * 64;
                 float fac[4];
