@@ -175,6 +175,36 @@ __device__ __forceinline__ int wave_max_u16(uint32_t v) {
     return __builtin_amdgcn_readlane(x, 63);
 }
 
+// Exchanges with lane ^ 16 and lane ^ 32 through gfx950's row swaps (VALU, no
+// LDS round trip): a swap of x with itself returns x and the partner's x in the
+// two halves of its result, in an order that depends on the lane.
+__device__ __forceinline__ float xmax16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xmax32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xsum16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xsum32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ int xsum16(int x) {
+    const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)x, (uint32_t)x, false, false);
+    return (int)(r[0] + r[1]);
+}
+// x of lane ^ 32: lanes 0-31 find it in the swapped source, lanes 32-63 in the
+// swapped destination
+__device__ __forceinline__ int xother32(int x) {
+    const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)x, (uint32_t)x, false, false);
+    return (int)((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 __device__ __forceinline__ float exp2_or_zero(float a, float b) {  // 2^(a-b), 0 when a = -inf
     return a == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(a - b);
 }
@@ -312,7 +342,7 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                     x[j] = use ? x[j] : 0.0f;
                     amax = fmaxf(amax, fabsf(x[j]));
                 }
-                amax = fmaxf(amax, __shfl_xor(amax, 16));  // the other 16 values of the block
+                amax = xmax16(amax);  // the other 16 values of the block
                 const float d = amax / 127.f;
                 const float id = amax != 0.0f ? 127.f / amax : 0.0f;
                 int sumq = 0;
@@ -329,11 +359,11 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                     w4[j] = w;
                 }
                 __builtin_memcpy(&my_bq[set], w4, 16);
-                sumq += __shfl_xor(sumq, 16);
+                sumq = xsum16(sumq);
                 const float dqv = (float)(_Float16)d * p.qscale;
                 const int civ = -8 * sumq;
-                const float dq2 = __shfl_xor(dqv, 32);  // inactive lanes: column n lives in lane ^ 32
-                const int ci2 = __shfl_xor(civ, 32);
+                const float dq2 = __int_as_float(xother32(__float_as_int(dqv)));  // inactive lanes: column n lives in lane ^ 32
+                const int ci2 = xother32(civ);
                 my_dq[set] = q_active ? dqv : dq2;
                 my_ci[set] = q_active ? civ : ci2;
             }
@@ -490,8 +520,7 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             float mu = m_ref;
             if (need) {
                 float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-                mt = fmaxf(mt, __shfl_xor(mt, 16));
-                mt = fmaxf(mt, __shfl_xor(mt, 32));
+                mt = xmax32(xmax16(mt));
                 mu = fmaxf(m_ref, mt);
             }
             m_used = mu;
@@ -532,8 +561,7 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         }
 
         // ---------------- this split's softmax statistics ------------------------
-        l_acc += __shfl_xor(l_acc, 16);
-        l_acc += __shfl_xor(l_acc, 32);
+        l_acc = xsum32(xsum16(l_acc));
         if (g == 0 && row_writer) lbuf[wq * 16 + my_r] = l_acc;
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (wq == 0 && g == 0 && row_writer && my_ok) {
