@@ -57,16 +57,17 @@ __device__ __forceinline__ float h2f(uint32_t bits) {
 template <bool GATE, bool VEC>
 __global__ __launch_bounds__(256) void op_prep_kernel(const char *__restrict__ x, int64_t x_nb1,
                                                       const char *__restrict__ gate, int64_t g_nb1, int K, int M,
-                                                      int M16, uint16_t *__restrict__ xh, uint16_t *__restrict__ xl,
-                                                      float *__restrict__ S) {
-    const int subs = K / 32;
+                                                      int Mp, int nq, uint16_t *__restrict__ xh,
+                                                      uint16_t *__restrict__ xl, float *__restrict__ S,
+                                                      uint16_t *__restrict__ sp) {
+    const int subs = K / 32, psubs = 32 * nq;  // sub-blocks, padded to whole groups of 4 super-blocks
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (int64_t)subs * M16) return;
-    const int t = (int)(idx / subs), s = (int)(idx - (int64_t)t * subs);
+    if (idx >= (int64_t)psubs * Mp) return;
+    const int t = (int)(idx / psubs), s = (int)(idx - (int64_t)t * psubs);
     float v[32], gv[32];
 #pragma unroll
     for (int j = 0; j < 32; ++j) v[j] = gv[j] = 0.0f;
-    if (t < M) {
+    if (t < M && s < subs) {
         const float *xr = reinterpret_cast<const float *>(x + t * x_nb1) + 32 * s;
         const float *gr = GATE ? reinterpret_cast<const float *>(gate + t * g_nb1) + 32 * s : nullptr;
         if (VEC) {
@@ -104,6 +105,20 @@ __global__ __launch_bounds__(256) void op_prep_kernel(const char *__restrict__ x
         __builtin_memcpy(&hb[j], &h, 2);
         __builtin_memcpy(&lb[j], &l, 2);
     }
+    // S hi + lo in the slot order of the min MFMA: group q of 4 super-blocks,
+    // slot 8g + e = sub-block 2g + (e & 1) of super-block 4q + (e >> 1)
+    {
+        const int sb = s >> 3, sub = s & 7;
+        const int slot = 8 * (sub >> 1) + 2 * (sb & 3) + (sub & 1);
+        float a = sum;
+        asm volatile("" : "+v"(a));
+        const _Float16 h = (_Float16)a;
+        const _Float16 l = (_Float16)(a - (float)h);
+        uint16_t *o = sp + ((int64_t)t * nq + (sb >> 2)) * 64 + slot;
+        __builtin_memcpy(o, &h, 2);
+        __builtin_memcpy(o + 32, &l, 2);
+    }
+    if (s >= subs) return;
     uint4 *ho = reinterpret_cast<uint4 *>(xh + (int64_t)t * K + 32 * s);
     uint4 *lo = reinterpret_cast<uint4 *>(xl + (int64_t)t * K + 32 * s);
 #pragma unroll
@@ -114,7 +129,7 @@ __global__ __launch_bounds__(256) void op_prep_kernel(const char *__restrict__ x
         ho[c] = a;
         lo[c] = b;
     }
-    S[idx] = sum;  // [token][sub-block]
+    S[(int64_t)t * subs + s] = sum;  // [token][sub-block]
 }
 
 // ---------------------------------------------------------------- op_gemm
@@ -278,6 +293,276 @@ __global__ __launch_bounds__(64 * KS) void op_gemm_kernel(GemmParams p) {
     }
 }
 
+// ---------------------------------------------------------------- op_gemm2
+// Larger token counts: a workgroup of 4 wavefronts owns 128 rows of W
+// (wavefront w: rows 32w..32w+31, two row tiles of 16) and 32 tokens (two
+// token tiles of 16).
+//   * Per super-block and row tile, the A operand of sub-block s is code *
+//     scale_s as an fp16 subnormal: an integer of at most 15 * 63 = 945, i.e.
+//     exactly code * scale * 2^-24 (one v_mul_u32_u24 scales the two codes of a
+//     dword, as the halves cannot carry into each other). The 8 sub-blocks then
+//     accumulate into one MFMA chain C = 2^-24 sum_k scale * code * x against x
+//     hi and lo, and acc += d 2^24 C once per super-block.
+//   * The min term sum_sb dmin * sum_s min_s * S_s runs on the MFMA as well:
+//     A = dmin * min as an fp16 hi + lo pair (17 bits) against B = S hi + lo,
+//     where k slot 8g + e of a group of four super-blocks holds sub-block
+//     2g + (e & 1) of super-block 4q + (e >> 1), so that each lane fills its
+//     two slots from the super-block it already holds.
+//   * Everything comes HBM -> LDS by DMA, double buffered: half a super-block
+//     of activations (128 values x 32 tokens, hi and lo: 16 KB, chunk c of
+//     token row t at c ^ (t & 15)), the 128 weight rows' super-block (18 KB)
+//     and, once per group of four super-blocks, the S hi/lo slots (4 KB).
+constexpr int kG2Rows = 128;
+constexpr int kG2Tok = 32;
+constexpr int kG2Half = kG2Tok * 512;        // activation bytes of half a super-block
+constexpr int kG2WBytes = kG2Rows * kBlockBytes;  // 18432
+constexpr int kG2WInst = kG2WBytes / 1024;   // 18 DMA instructions
+constexpr int kG2SBytes = kG2Tok * 128;      // S slots of one group: [32 tokens][hi 64 B | lo 64 B]
+static_assert(kG2WBytes % 1024 == 0, "weight stage in whole DMA instructions");
+
+// 16 bytes per lane from sbase + voff into LDS at m0 + 16 * lane, asynchronously
+// (the caller waits with s_waitcnt vmcnt); sbase and m0 are wave-uniform.
+__device__ __forceinline__ void dma16(uint32_t voff, const void *sbase, uint32_t m0v) {
+    const uint64_t b = (uint64_t)(uintptr_t)sbase;
+    const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(b >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    const uint32_t ms = (uint32_t)__builtin_amdgcn_readfirstlane((int)m0v);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(bs), "s"(ms) : "memory");
+}
+
+struct Gemm2Params {
+    const uint8_t *w;
+    int64_t w_nb1;
+    const uint16_t *x;  // xh [Mp][K]; xl starts xl_off bytes later
+    uint32_t xl_off;
+    const uint16_t *sp;  // [Mp][nq][64] fp16 S hi (32 slots) then lo (32 slots)
+    int K, N, M, Mp, nq;
+    float *dst;
+    int64_t d_nb1;
+};
+
+constexpr int kG2Lds = 2 * kG2Half + 2 * kG2WBytes + kG2SBytes;  // 73728 bytes: dynamic LDS
+
+__global__ __launch_bounds__(256) void op_gemm2_kernel(Gemm2Params p) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint8_t(*xs)[kG2Half] = reinterpret_cast<uint8_t(*)[kG2Half]>(lds);
+    uint8_t(*wb)[kG2WBytes] = reinterpret_cast<uint8_t(*)[kG2WBytes]>(lds + 2 * kG2Half);
+    uint8_t *sb_lds = lds + 2 * kG2Half + 2 * kG2WBytes;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
+    const int row0 = blockIdx.x * kG2Rows;
+    const int t0 = blockIdx.y * kG2Tok;
+    const int nsb = p.K / kQK;
+    const uint32_t xs0 = (uint32_t)(uintptr_t)&xs[0][0], wb0 = (uint32_t)(uintptr_t)&wb[0][0];
+    const uint32_t sb0 = (uint32_t)(uintptr_t)&sb_lds[0];
+
+    // ---- DMA plans (wave-uniform bases, per-lane offsets) ----
+    // activations: instruction i = 4 * wave + r covers tokens 2i, 2i+1: lane ->
+    // token 2i + (lane >> 5), hi/lo (lane >> 4) & 1, LDS chunk lane & 15
+    auto issue_x = [&](int h, int buf) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = 4 * wave + r;
+            const int t = 2 * i + (lane >> 5);
+            const uint32_t off = (uint32_t)((lane >> 4) & 1) * p.xl_off +
+                                 (uint32_t)((t0 + t) * p.K + 128 * h) * 2u + 16u * (uint32_t)((lane & 15) ^ (t & 15));
+            dma16(off, p.x, xs0 + (uint32_t)(buf * kG2Half + 1024 * i));
+        }
+    };
+    // weights: chunk id = 64 * i + lane -> row id / 9, chunk id % 9 (rows past N
+    // read row 0 and are never stored)
+    uint32_t woff[5];
+#pragma unroll
+    for (int r = 0; r < 5; ++r) {
+        const int i = 4 * r + wave;
+        const int id = 64 * (i < kG2WInst ? i : 0) + lane;
+        const int row = id / 9, ch = id - 9 * (id / 9);
+        const int grow = row0 + row < p.N ? row0 + row : 0;
+        woff[r] = (uint32_t)((int64_t)grow * p.w_nb1) + 16u * (uint32_t)ch;
+    }
+    auto issue_w = [&](int sb, int buf) {
+#pragma unroll
+        for (int r = 0; r < 5; ++r) {
+            const int i = 4 * r + wave;
+            if (i < kG2WInst) dma16(woff[r], p.w + (int64_t)sb * kBlockBytes, wb0 + (uint32_t)(buf * kG2WBytes + 1024 * i));
+        }
+    };
+    // S slots of group q: wave w copies tokens 8w..8w+7 (128 bytes each)
+    auto issue_s = [&](int q) {
+        const int t = 8 * wave + (lane >> 3);
+        const uint32_t off = (uint32_t)(((t0 + t) * p.nq + q) * 128 + 16 * (lane & 7));
+        dma16(off, p.sp, sb0 + (uint32_t)(1024 * wave));
+    };
+
+    floatx4 acc[2][2], accm[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) acc[rt][tt] = accm[rt][tt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    uint32_t amh[2][4], aml[2][4];  // A of the min MFMA per row tile: slots 2u, 2u+1 in dword u
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) amh[rt][u] = aml[rt][u] = 0u;
+
+    issue_x(0, 0);
+    issue_w(0, 0);
+    issue_s(0);
+    for (int sb = 0; sb < nsb; ++sb) {
+        const int u = sb & 3;
+        const uint8_t *wcur = &wb[sb & 1][0];
+        int sc[2][8];
+        floatx4 dq[2];  // d 2^24 of C rows 4g..4g+3
+        floatx4 C[2][2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) C[rt][tt] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int h = 2 * sb + hh;
+            // this wavefront's DMAs have landed; the barrier publishes every
+            // wavefront's and retires the buffers the next DMAs overwrite
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (h + 1 < 2 * nsb) issue_x(h + 1, (h + 1) & 1);
+            if (hh == 0 && sb + 1 < nsb) issue_w(sb + 1, (sb + 1) & 1);
+            if (hh == 0 && u == 0 && sb > 0) issue_s(sb >> 2);
+            if (hh == 0) {
+                // scales of A row n (every sub-block), d of C rows 4g..4g+3, and
+                // this lane's two min slots (sub-blocks 2g, 2g+1)
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    const uint8_t *hrow = wcur + (32 * wave + 16 * rt + n) * kBlockBytes;
+                    const uint4 hd = *reinterpret_cast<const uint4 *>(hrow);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        int mn;
+                        scale_min(hd.y, hd.z, hd.w, e, sc[rt][e], mn);
+                    }
+                    int m0, m1, unused;
+                    scale_min(hd.y, hd.z, hd.w, 2 * g, unused, m0);
+                    scale_min(hd.y, hd.z, hd.w, 2 * g + 1, unused, m1);
+                    const float dmin = h2f(hd.x >> 16);
+                    float a0 = dmin * (float)m0, a1 = dmin * (float)m1;  // exact: 11 x 6 bits
+                    asm volatile("" : "+v"(a0), "+v"(a1));
+                    const _Float16 h0 = (_Float16)a0, h1 = (_Float16)a1;
+                    const _Float16 l0 = (_Float16)(a0 - (float)h0), l1 = (_Float16)(a1 - (float)h1);
+                    uint16_t b[4];
+                    __builtin_memcpy(&b[0], &h0, 2);
+                    __builtin_memcpy(&b[1], &h1, 2);
+                    __builtin_memcpy(&b[2], &l0, 2);
+                    __builtin_memcpy(&b[3], &l1, 2);
+                    const uint32_t hw = (uint32_t)b[0] | ((uint32_t)b[1] << 16);
+                    const uint32_t lw = (uint32_t)b[2] | ((uint32_t)b[3] << 16);
+#pragma unroll
+                    for (int uu = 0; uu < 4; ++uu) {
+                        amh[rt][uu] = u == uu ? hw : amh[rt][uu];
+                        aml[rt][uu] = u == uu ? lw : aml[rt][uu];
+                    }
+                    float dv[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        dv[i] = h2f(*reinterpret_cast<const uint16_t *>(wcur + (32 * wave + 16 * rt + 4 * g + i) * kBlockBytes));
+                    dq[rt] = floatx4{dv[0], dv[1], dv[2], dv[3]} * 16777216.0f;
+                }
+            }
+            const uint8_t *xb = &xs[h & 1][0];
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int j = 2 * hh + jj;  // code group: sub-blocks 2j (low nibbles), 2j+1 (high)
+                half8 alo[2], ahi[2];
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    const uint2 qv = *reinterpret_cast<const uint2 *>(wcur + (32 * wave + 16 * rt + n) * kBlockBytes +
+                                                                      16 + 32 * j + 8 * g);
+                    uint32_t sp4[4];  // bytes 2m, 2m+1 spread to the two halves of dword m
+                    sp4[0] = __builtin_amdgcn_perm(0u, qv.x, 0x0c010c00u);
+                    sp4[1] = __builtin_amdgcn_perm(0u, qv.x, 0x0c030c02u);
+                    sp4[2] = __builtin_amdgcn_perm(0u, qv.y, 0x0c010c00u);
+                    sp4[3] = __builtin_amdgcn_perm(0u, qv.y, 0x0c030c02u);
+                    uint32_t lo[4], hi[4];
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        lo[m] = __umul24(sp4[m] & 0x000F000Fu, (uint32_t)sc[rt][2 * j]);
+                        hi[m] = __umul24((sp4[m] >> 4) & 0x000F000Fu, (uint32_t)sc[rt][2 * j + 1]);
+                    }
+                    __builtin_memcpy(&alo[rt], lo, 16);
+                    __builtin_memcpy(&ahi[rt], hi, 16);
+                }
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const int tr = 16 * tt + n;
+                    const uint8_t *row = xb + 512 * tr;
+                    const int c0 = 8 * jj + g, c1 = 8 * jj + 4 + g;
+                    half8 bh0, bl0, bh1, bl1;
+                    {
+                        const uint4 a = *reinterpret_cast<const uint4 *>(row + 16 * (c0 ^ (tr & 15)));
+                        const uint4 b = *reinterpret_cast<const uint4 *>(row + 256 + 16 * (c0 ^ (tr & 15)));
+                        const uint4 c = *reinterpret_cast<const uint4 *>(row + 16 * (c1 ^ (tr & 15)));
+                        const uint4 d = *reinterpret_cast<const uint4 *>(row + 256 + 16 * (c1 ^ (tr & 15)));
+                        __builtin_memcpy(&bh0, &a, 16);
+                        __builtin_memcpy(&bl0, &b, 16);
+                        __builtin_memcpy(&bh1, &c, 16);
+                        __builtin_memcpy(&bl1, &d, 16);
+                    }
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt) {
+                        C[rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[rt], bh0, C[rt][tt], 0, 0, 0);
+                        C[rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[rt], bl0, C[rt][tt], 0, 0, 0);
+                        C[rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[rt], bh1, C[rt][tt], 0, 0, 0);
+                        C[rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[rt], bl1, C[rt][tt], 0, 0, 0);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[rt][tt][i] = fmaf(dq[rt][i], C[rt][tt][i], acc[rt][tt][i]);
+        // min MFMA at the end of a group of four super-blocks (or of K)
+        if (u == 3 || sb == nsb - 1) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const uint8_t *srow = sb_lds + 128 * (16 * tt + n);
+                const uint4 bhv = *reinterpret_cast<const uint4 *>(srow + 16 * g);
+                const uint4 blv = *reinterpret_cast<const uint4 *>(srow + 64 + 16 * g);
+                half8 bh, bl;
+                __builtin_memcpy(&bh, &bhv, 16);
+                __builtin_memcpy(&bl, &blv, 16);
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    half8 ah, al;
+                    __builtin_memcpy(&ah, amh[rt], 16);
+                    __builtin_memcpy(&al, aml[rt], 16);
+                    accm[rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, accm[rt][tt], 0, 0, 0);
+                    accm[rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, accm[rt][tt], 0, 0, 0);
+                    accm[rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, accm[rt][tt], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int uu = 0; uu < 4; ++uu) amh[rt][uu] = aml[rt][uu] = 0u;
+        }
+    }
+    // ---- out[token][rows 4g..4g+3] = acc - accm ----
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+        const int r = row0 + 32 * wave + 16 * rt;
+        if (r >= p.N) continue;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int t = t0 + 16 * tt + n;
+            if (t >= p.M) continue;
+            float *drow = reinterpret_cast<float *>(reinterpret_cast<char *>(p.dst) + (int64_t)t * p.d_nb1);
+            const floatx4 o = acc[rt][tt] - accm[rt][tt];
+            *reinterpret_cast<float4 *>(drow + r + 4 * g) = make_float4(o[0], o[1], o[2], o[3]);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- op_gemv
 // Decode and verify (M <= 4 tokens, MT = 1, 2 or 4 slots): one workgroup of 256
 // threads takes 8 rows of W; thread (row, l32) takes half h = l32 & 1 (code
@@ -402,12 +687,28 @@ __global__ __launch_bounds__(256) void op_gemv_kernel(const uint8_t *__restrict_
 
 size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Workspace of the GEMM path: tokens padded to Mp (a multiple of 32), xh and xl
+// [Mp][K] fp16, S [Mp][K/32] f32, the S hi/lo slots [Mp][nq][64] fp16.
+struct OpLayout {
+    int64_t Mp, nq;
+    size_t xl, s, sp, total;
+};
+OpLayout op_layout(int64_t K, int64_t M) {
+    OpLayout l;
+    l.Mp = (M + kG2Tok - 1) / kG2Tok * kG2Tok;
+    l.nq = (K / kQK + 3) / 4;
+    l.xl = al256((size_t)(l.Mp * K) * 2);
+    l.s = 2 * l.xl;
+    l.sp = l.s + al256((size_t)(l.Mp * (K / 32)) * 4);
+    l.total = l.sp + al256((size_t)(l.Mp * l.nq * 64) * 2) + 256;
+    return l;
+}
+
 }  // namespace
 
 size_t out_proj_workspace(int64_t K, int64_t M) {
     if (M <= kGemvTokens) return 0;  // the decode path keeps its operands in LDS
-    const int64_t M16 = (M + 15) / 16 * 16;
-    return 2 * al256((size_t)(M16 * K) * 2) + al256((size_t)(K / 32 * M16) * 4) + 256;
+    return op_layout(K, M).total;
 }
 
 int launch_out_proj(const sqa_tensor &w, const sqa_tensor &x, const sqa_tensor *gate, const sqa_tensor &dst,
@@ -444,48 +745,81 @@ int launch_out_proj(const sqa_tensor &w, const sqa_tensor &x, const sqa_tensor *
         profile_stop(prof, s);
         return hip_status(hipGetLastError(), "out_proj launch");
     }
-    const int64_t M16 = (M + 15) / 16 * 16;
-    const size_t need = out_proj_workspace(K, M);
+    const OpLayout L = op_layout(K, M);
+    const size_t need = L.total;
     if (!ws || ws_bytes < need)
         return set_error(SQA_ERR_WORKSPACE, "out_proj: workspace %zu bytes < %zu needed", ws_bytes, need);
     uint8_t *base = reinterpret_cast<uint8_t *>(((uintptr_t)ws + 255) & ~(uintptr_t)255);
     uint16_t *xh = reinterpret_cast<uint16_t *>(base);
-    uint16_t *xl = reinterpret_cast<uint16_t *>(base + al256((size_t)(M16 * K) * 2));
-    float *S = reinterpret_cast<float *>(base + 2 * al256((size_t)(M16 * K) * 2));
+    uint16_t *xl = reinterpret_cast<uint16_t *>(base + L.xl);
+    float *S = reinterpret_cast<float *>(base + L.s);
+    uint16_t *sp = reinterpret_cast<uint16_t *>(base + L.sp);
+    // op_gemm2 once there are enough 32-token tiles to fill the chip; its DMA
+    // offsets are 32-bit
+    const bool big = M > 64 && (uint64_t)L.xl * 2 < (1ull << 32) && (uint64_t)N * w.nb[1] < (1ull << 32);
+    if (big) {
+        static std::once_flag g2_once;
+        static hipError_t g2_err = hipSuccess;
+        std::call_once(g2_once, [] {
+            g2_err = hipFuncSetAttribute((const void *)op_gemm2_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         kG2Lds);
+        });
+        if (g2_err != hipSuccess) return hip_status(g2_err, "out_proj LDS attribute");
+    }
 
     const int prof = profile_start("out_proj", s);
-    const int64_t nprep = K / 32 * M16;
+    const int64_t nprep = 32 * L.nq * L.Mp;
     const bool vec = (uintptr_t)x.data % 16 == 0 && x.nb[1] % 16 == 0 &&
                      (!gate || ((uintptr_t)gate->data % 16 == 0 && gate->nb[1] % 16 == 0));
     const dim3 pg((unsigned)((nprep + 255) / 256));
     const char *xd = (const char *)x.data, *gd = gate ? (const char *)gate->data : nullptr;
     const int64_t xn = (int64_t)x.nb[1], gn = gate ? (int64_t)gate->nb[1] : 0;
+    const int Ki = (int)K, Mi = (int)M, Mpi = (int)L.Mp, nqi = (int)L.nq;
     if (gate && vec)
-        op_prep_kernel<true, true><<<pg, dim3(256), 0, s>>>(xd, xn, gd, gn, (int)K, (int)M, (int)M16, xh, xl, S);
+        op_prep_kernel<true, true><<<pg, dim3(256), 0, s>>>(xd, xn, gd, gn, Ki, Mi, Mpi, nqi, xh, xl, S, sp);
     else if (gate)
-        op_prep_kernel<true, false><<<pg, dim3(256), 0, s>>>(xd, xn, gd, gn, (int)K, (int)M, (int)M16, xh, xl, S);
+        op_prep_kernel<true, false><<<pg, dim3(256), 0, s>>>(xd, xn, gd, gn, Ki, Mi, Mpi, nqi, xh, xl, S, sp);
     else if (vec)
-        op_prep_kernel<false, true><<<pg, dim3(256), 0, s>>>(xd, xn, gd, gn, (int)K, (int)M, (int)M16, xh, xl, S);
+        op_prep_kernel<false, true><<<pg, dim3(256), 0, s>>>(xd, xn, gd, gn, Ki, Mi, Mpi, nqi, xh, xl, S, sp);
     else
-        op_prep_kernel<false, false><<<pg, dim3(256), 0, s>>>(xd, xn, gd, gn, (int)K, (int)M, (int)M16, xh, xl, S);
-    GemmParams p;
-    p.w = (const uint8_t *)w.data;
-    p.w_nb1 = (int64_t)w.nb[1];
-    p.xh = xh;
-    p.xl = xl;
-    p.S = S;
-    p.K = (int)K;
-    p.N = (int)N;
-    p.M = (int)M;
-    p.M16 = (int)M16;
-    p.dst = (float *)dst.data;
-    p.d_nb1 = (int64_t)dst.nb[1];
-    // one 16-token tile per workgroup; for decode (one token tile) 16 rows and 16
-    // wavefronts that take one super-block each, else 64 rows and 4 wavefronts
-    if (M16 == 16 || N % 64 != 0)
-        op_gemm_kernel<16, 1><<<dim3((unsigned)(N / 16), (unsigned)(M16 / 16)), dim3(1024), 0, s>>>(p);
-    else
-        op_gemm_kernel<4, 4><<<dim3((unsigned)(N / 64), (unsigned)(M16 / 16)), dim3(256), 0, s>>>(p);
+        op_prep_kernel<false, false><<<pg, dim3(256), 0, s>>>(xd, xn, gd, gn, Ki, Mi, Mpi, nqi, xh, xl, S, sp);
+    if (big) {
+        Gemm2Params q;
+        q.w = (const uint8_t *)w.data;
+        q.w_nb1 = (int64_t)w.nb[1];
+        q.x = xh;
+        q.xl_off = (uint32_t)L.xl;
+        q.sp = sp;
+        q.K = Ki;
+        q.N = (int)N;
+        q.M = Mi;
+        q.Mp = Mpi;
+        q.nq = nqi;
+        q.dst = (float *)dst.data;
+        q.d_nb1 = (int64_t)dst.nb[1];
+        op_gemm2_kernel<<<dim3((unsigned)((N + kG2Rows - 1) / kG2Rows), (unsigned)(L.Mp / kG2Tok)), dim3(256), kG2Lds,
+                          s>>>(q);
+    } else {
+        const int64_t M16 = (M + 15) / 16 * 16;
+        GemmParams p;
+        p.w = (const uint8_t *)w.data;
+        p.w_nb1 = (int64_t)w.nb[1];
+        p.xh = xh;
+        p.xl = xl;
+        p.S = S;
+        p.K = Ki;
+        p.N = (int)N;
+        p.M = Mi;
+        p.M16 = (int)M16;
+        p.dst = (float *)dst.data;
+        p.d_nb1 = (int64_t)dst.nb[1];
+        // one 16-token tile per workgroup; for decode (one token tile) 16 rows and
+        // 16 wavefronts that take one super-block each, else 64 rows and 4 wavefronts
+        if (M16 == 16 || N % 64 != 0)
+            op_gemm_kernel<16, 1><<<dim3((unsigned)(N / 16), (unsigned)(M16 / 16)), dim3(1024), 0, s>>>(p);
+        else
+            op_gemm_kernel<4, 4><<<dim3((unsigned)(N / 64), (unsigned)(M16 / 16)), dim3(256), 0, s>>>(p);
+    }
     profile_stop(prof, s);
     return hip_status(hipGetLastError(), "out_proj launch");
 }

@@ -60,10 +60,17 @@ def test_out_proj_without_gate(sqa, orc, dev, M):
     assert run(sqa, orc, dev, 512, 4096, M, 200 + M, gate=False) <= TOL
 
 
-@pytest.mark.parametrize("N,K,M", [(48, 256, 1), (48, 256, 33), (16, 512, 7), (80, 1024, 70)])
+@pytest.mark.parametrize("N,K,M", [(48, 256, 1), (48, 256, 33), (16, 512, 7), (80, 1024, 70), (48, 1280, 65),
+                                   (2064, 768, 97), (2048, 4096, 1000)])
 def test_out_proj_small_and_ragged_shapes(sqa, orc, dev, N, K, M):
-    # one super-block (three of the four K quarters idle), N not a multiple of 64
+    # one super-block, N not a multiple of 64 or 128 (row tiles past N), K of 3
+    # or 5 super-blocks (a partial group of four for the min term), token counts
+    # that are not a multiple of 32
     assert run(sqa, orc, dev, N, K, M, 300 + N + M) <= TOL
+
+
+def test_out_proj_large_ubatch_without_gate(sqa, orc, dev):
+    assert run(sqa, orc, dev, 512, 4096, 2048, 17, gate=False) <= TOL
 
 
 def test_out_proj_rejects_unsupported_shapes(sqa, dev):
