@@ -53,26 +53,32 @@ __device__ __forceinline__ float h2f(uint32_t bits) {
 }
 
 // ---------------------------------------------------------------- op_prep
-// x (and gate) rows: 16-byte aligned when VEC (checked on the host)
+// One thread per 8 values (a quarter sub-block) of one token: xg = x *
+// sigmoid(gate) as an fp16 hi + lo pair, and through the lane quad the
+// sub-block sum S (f32) and its hi + lo slots for the min MFMA of op_gemm2.
+// Tokens M..Mp-1 and the sub-blocks that pad K to whole groups of four
+// super-blocks are zeros. x (and gate) rows are 16-byte aligned when VEC.
 template <bool GATE, bool VEC>
 __global__ __launch_bounds__(256) void op_prep_kernel(const char *__restrict__ x, int64_t x_nb1,
                                                       const char *__restrict__ gate, int64_t g_nb1, int K, int M,
                                                       int Mp, int nq, uint16_t *__restrict__ xh,
                                                       uint16_t *__restrict__ xl, float *__restrict__ S,
                                                       uint16_t *__restrict__ sp) {
-    const int subs = K / 32, psubs = 32 * nq;  // sub-blocks, padded to whole groups of 4 super-blocks
+    const int subs = K / 32, psubs = 32 * nq;
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (int64_t)psubs * Mp) return;
-    const int t = (int)(idx / psubs), s = (int)(idx - (int64_t)t * psubs);
-    float v[32], gv[32];
+    if (idx >= (int64_t)Mp * psubs * 4) return;  // whole quads: the total is a multiple of 4
+    const int qtr = (int)(idx & 3);
+    const int64_t ts = idx >> 2;
+    const int t = (int)(ts / psubs), s = (int)(ts - (int64_t)t * psubs);
+    float v[8], gv[8];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) v[j] = gv[j] = 0.0f;
+    for (int j = 0; j < 8; ++j) v[j] = gv[j] = 0.0f;
     if (t < M && s < subs) {
-        const float *xr = reinterpret_cast<const float *>(x + t * x_nb1) + 32 * s;
-        const float *gr = GATE ? reinterpret_cast<const float *>(gate + t * g_nb1) + 32 * s : nullptr;
+        const float *xr = reinterpret_cast<const float *>(x + t * x_nb1) + 32 * s + 8 * qtr;
+        const float *gr = GATE ? reinterpret_cast<const float *>(gate + t * g_nb1) + 32 * s + 8 * qtr : nullptr;
         if (VEC) {
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
+            for (int c = 0; c < 2; ++c) {
                 const float4 a = reinterpret_cast<const float4 *>(xr)[c];
                 v[4 * c] = a.x, v[4 * c + 1] = a.y, v[4 * c + 2] = a.z, v[4 * c + 3] = a.w;
                 if (GATE) {
@@ -82,20 +88,20 @@ __global__ __launch_bounds__(256) void op_prep_kernel(const char *__restrict__ x
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < 32; ++j) {
+            for (int j = 0; j < 8; ++j) {
                 v[j] = xr[j];
                 if (GATE) gv[j] = gr[j];
             }
         }
         if (GATE) {
 #pragma unroll
-            for (int j = 0; j < 32; ++j) v[j] = v[j] * (1.0f / (1.0f + expf(-gv[j])));
+            for (int j = 0; j < 8; ++j) v[j] = v[j] * (1.0f / (1.0f + expf(-gv[j])));
         }
     }
     float sum = 0.0f;
-    uint16_t hb[32], lb[32];
+    uint16_t hb[8], lb[8];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
+    for (int j = 0; j < 8; ++j) {
         sum += v[j];
         float a = v[j];
         // opaque: one fp32 value feeds both the stored hi and the hi subtracted for lo
@@ -105,9 +111,12 @@ __global__ __launch_bounds__(256) void op_prep_kernel(const char *__restrict__ x
         __builtin_memcpy(&hb[j], &h, 2);
         __builtin_memcpy(&lb[j], &l, 2);
     }
-    // S hi + lo in the slot order of the min MFMA: group q of 4 super-blocks,
-    // slot 8g + e = sub-block 2g + (e & 1) of super-block 4q + (e >> 1)
-    {
+    // sum over the quad (quad_perm [1,0,3,2], then [2,3,0,1])
+    sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sum), 0xB1, 0xf, 0xf, false));
+    sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sum), 0x4E, 0xf, 0xf, false));
+    if (qtr == 0) {
+        // S hi + lo in the slot order of the min MFMA: group q of 4 super-blocks,
+        // slot 8g + e = sub-block 2g + (e & 1) of super-block 4q + (e >> 1)
         const int sb = s >> 3, sub = s & 7;
         const int slot = 8 * (sub >> 1) + 2 * (sb & 3) + (sub & 1);
         float a = sum;
@@ -117,19 +126,14 @@ __global__ __launch_bounds__(256) void op_prep_kernel(const char *__restrict__ x
         uint16_t *o = sp + ((int64_t)t * nq + (sb >> 2)) * 64 + slot;
         __builtin_memcpy(o, &h, 2);
         __builtin_memcpy(o + 32, &l, 2);
+        if (s < subs) S[(int64_t)t * subs + s] = sum;  // [token][sub-block]
     }
     if (s >= subs) return;
-    uint4 *ho = reinterpret_cast<uint4 *>(xh + (int64_t)t * K + 32 * s);
-    uint4 *lo = reinterpret_cast<uint4 *>(xl + (int64_t)t * K + 32 * s);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        uint4 a, b;
-        __builtin_memcpy(&a, hb + 8 * c, 16);
-        __builtin_memcpy(&b, lb + 8 * c, 16);
-        ho[c] = a;
-        lo[c] = b;
-    }
-    S[(int64_t)t * subs + s] = sum;  // [token][sub-block]
+    uint4 a, b;
+    __builtin_memcpy(&a, hb, 16);
+    __builtin_memcpy(&b, lb, 16);
+    *reinterpret_cast<uint4 *>(xh + (int64_t)t * K + 32 * s + 8 * qtr) = a;
+    *reinterpret_cast<uint4 *>(xl + (int64_t)t * K + 32 * s + 8 * qtr) = b;
 }
 
 // ---------------------------------------------------------------- op_gemm
@@ -294,9 +298,8 @@ __global__ __launch_bounds__(64 * KS) void op_gemm_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------- op_gemm2
-// Larger token counts: a workgroup of 4 wavefronts owns 128 rows of W
-// (wavefront w: rows 32w..32w+31, two row tiles of 16) and 32 tokens (two
-// token tiles of 16).
+// Larger token counts: a workgroup of 8 wavefronts owns 128 rows of W
+// (wavefront w: rows 16w..16w+15) and 32 tokens (two token tiles of 16).
 //   * Per super-block and row tile, the A operand of sub-block s is code *
 //     scale_s as an fp16 subnormal: an integer of at most 15 * 63 = 945, i.e.
 //     exactly code * scale * 2^-24 (one v_mul_u32_u24 scales the two codes of a
@@ -311,14 +314,39 @@ __global__ __launch_bounds__(64 * KS) void op_gemm_kernel(GemmParams p) {
 //   * Everything comes HBM -> LDS by DMA, double buffered: half a super-block
 //     of activations (128 values x 32 tokens, hi and lo: 16 KB, chunk c of
 //     token row t at c ^ (t & 15)), the 128 weight rows' super-block (18 KB)
-//     and, once per group of four super-blocks, the S hi/lo slots (4 KB).
+//     and, one group of four super-blocks ahead, the S hi/lo slots (4 KB).
+//     Each wait counts the wavefront's younger DMAs, so the stages in flight
+//     are not waited for.
 constexpr int kG2Rows = 128;
 constexpr int kG2Tok = 32;
+constexpr int kG2RT = 1;                            // row tiles of 16 per wavefront
+constexpr int kG2Waves = kG2Rows / (16 * kG2RT);   // 8: two wavefronts per SIMD
+constexpr int kG2XInst = 16 / kG2Waves;             // activation DMA instructions per wavefront
 constexpr int kG2Half = kG2Tok * 512;        // activation bytes of half a super-block
 constexpr int kG2WBytes = kG2Rows * kBlockBytes;  // 18432
 constexpr int kG2WInst = kG2WBytes / 1024;   // 18 DMA instructions
+constexpr int kG2WPer = (kG2WInst + kG2Waves - 1) / kG2Waves;
 constexpr int kG2SBytes = kG2Tok * 128;      // S slots of one group: [32 tokens][hi 64 B | lo 64 B]
+constexpr int kG2XAhead = 1;                  // activation halves in flight ahead of the one in use
+constexpr int kG2WAhead = 1;                  // weight super-blocks in flight ahead of the one in use
+constexpr int kG2XBufs = kG2XAhead + 1;
+constexpr int kG2WBufs = kG2WAhead + 1;
+static_assert(2 * kG2WAhead >= kG2XAhead, "a weight stage is issued no later than the activations of its first half");
 static_assert(kG2WBytes % 1024 == 0, "weight stage in whole DMA instructions");
+
+// Wait until at most n vector-memory loads of this wavefront are outstanding and
+// its LDS accesses are done, then synchronise the workgroup (n wave-uniform).
+__device__ __forceinline__ void wait_vm_barrier(int n) {
+    switch (__builtin_amdgcn_readfirstlane(n)) {
+#define SQA_WAIT_CASE(N) \
+    case N: asm volatile("s_waitcnt vmcnt(" #N ") lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+        SQA_WAIT_CASE(0) SQA_WAIT_CASE(1) SQA_WAIT_CASE(2) SQA_WAIT_CASE(3) SQA_WAIT_CASE(4)
+        SQA_WAIT_CASE(5) SQA_WAIT_CASE(6) SQA_WAIT_CASE(7) SQA_WAIT_CASE(8) SQA_WAIT_CASE(9)
+        SQA_WAIT_CASE(10) SQA_WAIT_CASE(11) SQA_WAIT_CASE(12) SQA_WAIT_CASE(13) SQA_WAIT_CASE(14)
+#undef SQA_WAIT_CASE
+        default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
+    }
+}
 
 // 16 bytes per lane from sbase + voff into LDS at m0 + 16 * lane, asynchronously
 // (the caller waits with s_waitcnt vmcnt); sbase and m0 are wave-uniform.
@@ -341,13 +369,15 @@ struct Gemm2Params {
     int64_t d_nb1;
 };
 
-constexpr int kG2Lds = 2 * kG2Half + 2 * kG2WBytes + kG2SBytes;  // 73728 bytes: dynamic LDS
+// 77824 bytes of dynamic LDS: two workgroups per CU (deeper rings measured slower,
+// 48 vs 36 us at 512 tokens, as they halve the workgroups a CU holds)
+constexpr int kG2Lds = kG2XBufs * kG2Half + kG2WBufs * kG2WBytes + 2 * kG2SBytes;
 
-__global__ __launch_bounds__(256) void op_gemm2_kernel(Gemm2Params p) {
+__global__ __launch_bounds__(64 * kG2Waves) void op_gemm2_kernel(Gemm2Params p) {
     extern __shared__ __align__(16) uint8_t lds[];
     uint8_t(*xs)[kG2Half] = reinterpret_cast<uint8_t(*)[kG2Half]>(lds);
-    uint8_t(*wb)[kG2WBytes] = reinterpret_cast<uint8_t(*)[kG2WBytes]>(lds + 2 * kG2Half);
-    uint8_t *sb_lds = lds + 2 * kG2Half + 2 * kG2WBytes;
+    uint8_t(*wb)[kG2WBytes] = reinterpret_cast<uint8_t(*)[kG2WBytes]>(lds + kG2XBufs * kG2Half);
+    uint8_t *sb_lds = lds + kG2XBufs * kG2Half + kG2WBufs * kG2WBytes;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
     const int row0 = blockIdx.x * kG2Rows;
@@ -357,12 +387,12 @@ __global__ __launch_bounds__(256) void op_gemm2_kernel(Gemm2Params p) {
     const uint32_t sb0 = (uint32_t)(uintptr_t)&sb_lds[0];
 
     // ---- DMA plans (wave-uniform bases, per-lane offsets) ----
-    // activations: instruction i = 4 * wave + r covers tokens 2i, 2i+1: lane ->
+    // activations: instruction i = kG2XInst * wave + r covers tokens 2i, 2i+1: lane ->
     // token 2i + (lane >> 5), hi/lo (lane >> 4) & 1, LDS chunk lane & 15
     auto issue_x = [&](int h, int buf) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int i = 4 * wave + r;
+        for (int r = 0; r < kG2XInst; ++r) {
+            const int i = kG2XInst * wave + r;
             const int t = 2 * i + (lane >> 5);
             const uint32_t off = (uint32_t)((lane >> 4) & 1) * p.xl_off +
                                  (uint32_t)((t0 + t) * p.K + 128 * h) * 2u + 16u * (uint32_t)((lane & 15) ^ (t & 15));
@@ -371,10 +401,10 @@ __global__ __launch_bounds__(256) void op_gemm2_kernel(Gemm2Params p) {
     };
     // weights: chunk id = 64 * i + lane -> row id / 9, chunk id % 9 (rows past N
     // read row 0 and are never stored)
-    uint32_t woff[5];
+    uint32_t woff[kG2WPer];
 #pragma unroll
-    for (int r = 0; r < 5; ++r) {
-        const int i = 4 * r + wave;
+    for (int r = 0; r < kG2WPer; ++r) {
+        const int i = kG2Waves * r + wave;
         const int id = 64 * (i < kG2WInst ? i : 0) + lane;
         const int row = id / 9, ch = id - 9 * (id / 9);
         const int grow = row0 + row < p.N ? row0 + row : 0;
@@ -382,57 +412,83 @@ __global__ __launch_bounds__(256) void op_gemm2_kernel(Gemm2Params p) {
     }
     auto issue_w = [&](int sb, int buf) {
 #pragma unroll
-        for (int r = 0; r < 5; ++r) {
-            const int i = 4 * r + wave;
+        for (int r = 0; r < kG2WPer; ++r) {
+            const int i = kG2Waves * r + wave;
             if (i < kG2WInst) dma16(woff[r], p.w + (int64_t)sb * kBlockBytes, wb0 + (uint32_t)(buf * kG2WBytes + 1024 * i));
         }
     };
-    // S slots of group q: wave w copies tokens 8w..8w+7 (128 bytes each)
+    // S slots of group q into buffer q & 1: wavefront w < 4 copies tokens
+    // 8w..8w+7 (128 bytes each)
     auto issue_s = [&](int q) {
+        if (wave >= kG2Tok / 8) return;
         const int t = 8 * wave + (lane >> 3);
         const uint32_t off = (uint32_t)(((t0 + t) * p.nq + q) * 128 + 16 * (lane & 7));
-        dma16(off, p.sp, sb0 + (uint32_t)(1024 * wave));
+        dma16(off, p.sp, sb0 + (uint32_t)((q & 1) * kG2SBytes + 1024 * wave));
     };
 
-    floatx4 acc[2][2], accm[2][2];
+    floatx4 acc[kG2RT][2], accm[kG2RT][2];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int rt = 0; rt < kG2RT; ++rt)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) acc[rt][tt] = accm[rt][tt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    uint32_t amh[2][4], aml[2][4];  // A of the min MFMA per row tile: slots 2u, 2u+1 in dword u
+    uint32_t amh[kG2RT][4], aml[kG2RT][4];  // A of the min MFMA per row tile: slots 2u, 2u+1 in dword u
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int rt = 0; rt < kG2RT; ++rt)
 #pragma unroll
         for (int u = 0; u < 4; ++u) amh[rt][u] = aml[rt][u] = 0u;
 
-    issue_x(0, 0);
-    issue_w(0, 0);
+    // Issue order: weights of super-blocks 0..kG2WAhead-1, S of group 0 and
+    // activation halves 0..kG2XAhead-1 first; then at the start of half k the
+    // weights of super-block k/2 + kG2WAhead (even k), the S of group k/8 + 1 (k a
+    // multiple of 8) and activation half k + kG2XAhead. A stage is read only after
+    // the wait for activation half h, and every DMA it needs was issued no later
+    // than that half's.
+    const int nh = 2 * nsb, ngrp = (nsb + 3) / 4;
+    const int n_w = (kG2WPer - 1) * kG2Waves + wave < kG2WInst ? kG2WPer : kG2WPer - 1;  // weight DMAs per stage
+    const int n_s = wave < kG2Tok / 8 ? 1 : 0;
+    auto issued_in_half = [&](int k) -> int {
+        int c = 0;
+        if ((k & 1) == 0 && (k >> 1) + kG2WAhead < nsb) c += n_w;
+        if ((k & 7) == 0 && (k >> 3) + 1 < ngrp) c += n_s;
+        if (k + kG2XAhead < nh) c += kG2XInst;
+        return c;
+    };
+    // this wavefront's DMAs issued after activation half h
+    auto younger_than = [&](int h) -> int {
+        const int k0 = h - kG2XAhead;
+        int y = 0;
+        if (k0 < 0) y += ((nh < kG2XAhead ? nh : kG2XAhead) - 1 - h) * kG2XInst;  // later prologue halves
+        for (int k = k0 + 1 > 0 ? k0 + 1 : 0; k < h; ++k) y += issued_in_half(k);
+        return y;
+    };
+    for (int sb = 0; sb < kG2WAhead && sb < nsb; ++sb) issue_w(sb, sb);
     issue_s(0);
+    for (int k = 0; k < kG2XAhead && k < nh; ++k) issue_x(k, k);
     for (int sb = 0; sb < nsb; ++sb) {
         const int u = sb & 3;
-        const uint8_t *wcur = &wb[sb & 1][0];
-        int sc[2][8];
-        floatx4 dq[2];  // d 2^24 of C rows 4g..4g+3
-        floatx4 C[2][2];
+        const uint8_t *wcur = &wb[sb % kG2WBufs][0];
+        int sc[kG2RT][8];
+        floatx4 dq[kG2RT];  // d 2^24 of C rows 4g..4g+3
+        floatx4 C[kG2RT][2];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+        for (int rt = 0; rt < kG2RT; ++rt)
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) C[rt][tt] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int h = 2 * sb + hh;
-            // this wavefront's DMAs have landed; the barrier publishes every
-            // wavefront's and retires the buffers the next DMAs overwrite
-            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            if (h + 1 < 2 * nsb) issue_x(h + 1, (h + 1) & 1);
-            if (hh == 0 && sb + 1 < nsb) issue_w(sb + 1, (sb + 1) & 1);
-            if (hh == 0 && u == 0 && sb > 0) issue_s(sb >> 2);
+            // this wavefront's DMAs for half h have landed; the barrier publishes
+            // every wavefront's and retires the buffers the next DMAs overwrite
+            wait_vm_barrier(younger_than(h));
+            if (hh == 0 && sb + kG2WAhead < nsb) issue_w(sb + kG2WAhead, (sb + kG2WAhead) % kG2WBufs);
+            if (hh == 0 && u == 0 && (sb >> 2) + 1 < ngrp) issue_s((sb >> 2) + 1);
+            if (h + kG2XAhead < nh) issue_x(h + kG2XAhead, (h + kG2XAhead) % kG2XBufs);
             if (hh == 0) {
                 // scales of A row n (every sub-block), d of C rows 4g..4g+3, and
                 // this lane's two min slots (sub-blocks 2g, 2g+1)
 #pragma unroll
-                for (int rt = 0; rt < 2; ++rt) {
-                    const uint8_t *hrow = wcur + (32 * wave + 16 * rt + n) * kBlockBytes;
+                for (int rt = 0; rt < kG2RT; ++rt) {
+                    const uint8_t *hrow = wcur + (16 * kG2RT * wave + 16 * rt + n) * kBlockBytes;
                     const uint4 hd = *reinterpret_cast<const uint4 *>(hrow);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
@@ -462,18 +518,18 @@ __global__ __launch_bounds__(256) void op_gemm2_kernel(Gemm2Params p) {
                     float dv[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        dv[i] = h2f(*reinterpret_cast<const uint16_t *>(wcur + (32 * wave + 16 * rt + 4 * g + i) * kBlockBytes));
+                        dv[i] = h2f(*reinterpret_cast<const uint16_t *>(wcur + (16 * kG2RT * wave + 16 * rt + 4 * g + i) * kBlockBytes));
                     dq[rt] = floatx4{dv[0], dv[1], dv[2], dv[3]} * 16777216.0f;
                 }
             }
-            const uint8_t *xb = &xs[h & 1][0];
+            const uint8_t *xb = &xs[h % kG2XBufs][0];
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) {
                 const int j = 2 * hh + jj;  // code group: sub-blocks 2j (low nibbles), 2j+1 (high)
-                half8 alo[2], ahi[2];
+                half8 alo[kG2RT], ahi[kG2RT];
 #pragma unroll
-                for (int rt = 0; rt < 2; ++rt) {
-                    const uint2 qv = *reinterpret_cast<const uint2 *>(wcur + (32 * wave + 16 * rt + n) * kBlockBytes +
+                for (int rt = 0; rt < kG2RT; ++rt) {
+                    const uint2 qv = *reinterpret_cast<const uint2 *>(wcur + (16 * kG2RT * wave + 16 * rt + n) * kBlockBytes +
                                                                       16 + 32 * j + 8 * g);
                     uint32_t sp4[4];  // bytes 2m, 2m+1 spread to the two halves of dword m
                     sp4[0] = __builtin_amdgcn_perm(0u, qv.x, 0x0c010c00u);
@@ -506,7 +562,7 @@ __global__ __launch_bounds__(256) void op_gemm2_kernel(Gemm2Params p) {
                         __builtin_memcpy(&bl1, &d, 16);
                     }
 #pragma unroll
-                    for (int rt = 0; rt < 2; ++rt) {
+                    for (int rt = 0; rt < kG2RT; ++rt) {
                         C[rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[rt], bh0, C[rt][tt], 0, 0, 0);
                         C[rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[rt], bl0, C[rt][tt], 0, 0, 0);
                         C[rt][tt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[rt], bh1, C[rt][tt], 0, 0, 0);
@@ -516,7 +572,7 @@ __global__ __launch_bounds__(256) void op_gemm2_kernel(Gemm2Params p) {
             }
         }
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+        for (int rt = 0; rt < kG2RT; ++rt)
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -525,14 +581,14 @@ __global__ __launch_bounds__(256) void op_gemm2_kernel(Gemm2Params p) {
         if (u == 3 || sb == nsb - 1) {
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
-                const uint8_t *srow = sb_lds + 128 * (16 * tt + n);
+                const uint8_t *srow = sb_lds + ((sb >> 2) & 1) * kG2SBytes + 128 * (16 * tt + n);
                 const uint4 bhv = *reinterpret_cast<const uint4 *>(srow + 16 * g);
                 const uint4 blv = *reinterpret_cast<const uint4 *>(srow + 64 + 16 * g);
                 half8 bh, bl;
                 __builtin_memcpy(&bh, &bhv, 16);
                 __builtin_memcpy(&bl, &blv, 16);
 #pragma unroll
-                for (int rt = 0; rt < 2; ++rt) {
+                for (int rt = 0; rt < kG2RT; ++rt) {
                     half8 ah, al;
                     __builtin_memcpy(&ah, amh[rt], 16);
                     __builtin_memcpy(&al, aml[rt], 16);
@@ -542,15 +598,15 @@ __global__ __launch_bounds__(256) void op_gemm2_kernel(Gemm2Params p) {
                 }
             }
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
+            for (int rt = 0; rt < kG2RT; ++rt)
 #pragma unroll
                 for (int uu = 0; uu < 4; ++uu) amh[rt][uu] = aml[rt][uu] = 0u;
         }
     }
     // ---- out[token][rows 4g..4g+3] = acc - accm ----
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        const int r = row0 + 32 * wave + 16 * rt;
+    for (int rt = 0; rt < kG2RT; ++rt) {
+        const int r = row0 + 16 * kG2RT * wave + 16 * rt;
         if (r >= p.N) continue;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
@@ -768,7 +824,7 @@ int launch_out_proj(const sqa_tensor &w, const sqa_tensor &x, const sqa_tensor *
     }
 
     const int prof = profile_start("out_proj", s);
-    const int64_t nprep = 32 * L.nq * L.Mp;
+    const int64_t nprep = 4 * 32 * L.nq * L.Mp;
     const bool vec = (uintptr_t)x.data % 16 == 0 && x.nb[1] % 16 == 0 &&
                      (!gate || ((uintptr_t)gate->data % 16 == 0 && gate->nb[1] % 16 == 0));
     const dim3 pg((unsigned)((nprep + 255) / 256));
@@ -797,7 +853,7 @@ int launch_out_proj(const sqa_tensor &w, const sqa_tensor &x, const sqa_tensor *
         q.nq = nqi;
         q.dst = (float *)dst.data;
         q.d_nb1 = (int64_t)dst.nb[1];
-        op_gemm2_kernel<<<dim3((unsigned)((N + kG2Rows - 1) / kG2Rows), (unsigned)(L.Mp / kG2Tok)), dim3(256), kG2Lds,
+        op_gemm2_kernel<<<dim3((unsigned)((N + kG2Rows - 1) / kG2Rows), (unsigned)(L.Mp / kG2Tok)), dim3(64 * kG2Waves), kG2Lds,
                           s>>>(q);
     } else {
         const int64_t M16 = (M + 15) / 16 * 16;
