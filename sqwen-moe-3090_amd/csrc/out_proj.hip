@@ -380,8 +380,20 @@ __global__ __launch_bounds__(64 * kG2Waves) void op_gemm2_kernel(Gemm2Params p) 
     uint8_t *sb_lds = lds + kG2XBufs * kG2Half + kG2WBufs * kG2WBytes;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, g = lane >> 4, n = lane & 15;
-    const int row0 = blockIdx.x * kG2Rows;
-    const int t0 = blockIdx.y * kG2Tok;
+    // workgroups go round-robin to the 8 XCDs: give each XCD whole token tiles
+    // (every row block of them), so an XCD's L2 serves its activations to all
+    // its row blocks
+    int bx = (int)blockIdx.x, by = (int)blockIdx.y;
+    {
+        const int nx = (int)gridDim.x, ny = (int)gridDim.y;
+        if (ny % 8 == 0) {
+            const int id = bx + nx * by, k = id / 8;
+            by = (id % 8) * (ny / 8) + k / nx;
+            bx = k % nx;
+        }
+    }
+    const int row0 = bx * kG2Rows;
+    const int t0 = by * kG2Tok;
     const int nsb = p.K / kQK;
     const uint32_t xs0 = (uint32_t)(uintptr_t)&xs[0][0], wb0 = (uint32_t)(uintptr_t)&wb[0][0];
     const uint32_t sb0 = (uint32_t)(uintptr_t)&sb_lds[0];
