@@ -13,6 +13,7 @@ Tensor conventions (torch shapes, C order, all on the GPU):
   out     float32 (n_q, H, D)             [D, H, n_q] attention output
 """
 import ctypes
+import struct
 import os
 
 import torch
@@ -42,6 +43,9 @@ class SqaError(RuntimeError):
         self.status = status
 
 
+_TENSOR_LAYOUT = struct.Struct("<ii4q4QQ")  # type, pad_, ne[4], nb[4], data
+
+
 class Tensor(ctypes.Structure):
     """sqa_tensor: ggml's {type, ne[4], nb[4], data} (reference ffi.rs:22-39)."""
 
@@ -55,17 +59,12 @@ class Tensor(ctypes.Structure):
 
     @staticmethod
     def make(ttype, ne, nb, ptr):
-        t = Tensor()
-        t.type = ttype
-        ne = list(ne) + [1] * (4 - len(ne))
+        """Fields packed in one go: a decode step builds five of these per call."""
+        ne = tuple(ne) + (1,) * (4 - len(ne))
         nb = list(nb)
         while len(nb) < 4:
             nb.append(nb[-1] * ne[len(nb) - 1])
-        for i in range(4):
-            t.ne[i] = int(ne[i])
-            t.nb[i] = int(nb[i])
-        t.data = int(ptr)
-        return t
+        return Tensor.from_buffer_copy(_TENSOR_LAYOUT.pack(ttype, 0, *ne, *nb, ptr))
 
 
 class Rope(ctypes.Structure):
@@ -290,9 +289,9 @@ def flash_attn_ext(q, k_cache, v_cache, n_kv, mask=None, scale=None, max_bias=0.
         out = torch.empty((n_q, H, D), dtype=torch.float32, device=q.device)
     tq, tk, tv = q_desc(q), cache_view(k_cache, n_kv), cache_view(v_cache, n_kv)
     to, tm = out_desc(out), mask_desc(mask)
-    need = int(lib().sqa_flash_attn_ext_workspace_size(ctypes.byref(tq), ctypes.byref(tk), ctypes.byref(tv),
-                                                       ctypes.byref(to)))
-    if workspace is None:
+    if workspace is None:  # a given workspace is checked by the library
+        need = int(lib().sqa_flash_attn_ext_workspace_size(ctypes.byref(tq), ctypes.byref(tk), ctypes.byref(tv),
+                                                           ctypes.byref(to)))
         workspace, _ = _workspace(need, q.device)
     wptr = workspace.data_ptr() if workspace is not None else None
     wbytes = workspace.numel() if workspace is not None else 0
@@ -329,9 +328,9 @@ def flash_attn_ext_causal(q, k_cache, v_cache, n_kv, q_pos0, gate=None, scale=No
     if gate is not None:
         s = gate.stride()
         tg = Tensor.make(TYPE_F32, [D, H, n_q, 1], [4, s[1] * 4, s[0] * 4], gate.data_ptr())
-    need = int(lib().sqa_flash_attn_ext_workspace_size(ctypes.byref(tq), ctypes.byref(tk), ctypes.byref(tv),
-                                                       ctypes.byref(to)))
-    if workspace is None:
+    if workspace is None:  # a given workspace is checked by the library
+        need = int(lib().sqa_flash_attn_ext_workspace_size(ctypes.byref(tq), ctypes.byref(tk), ctypes.byref(tv),
+                                                           ctypes.byref(to)))
         workspace, _ = _workspace(need, q.device)
     wptr = workspace.data_ptr() if workspace is not None else None
     wbytes = workspace.numel() if workspace is not None else 0
