@@ -238,62 +238,63 @@ __global__ __launch_bounds__(256) void kvprep_kernel(const uint8_t *__restrict__
     }
 }
 
-// One thread per 32-value block of one (query, head) row: q8_0 with ggml's x86
-// rounding (d = amax/127, codes = rint(x * 127/amax)), then Q' = code * qd with
-// qd = fp16(d) * scale * log2(e) in fp32, written as fp16 hi = fp16(Q') and
-// lo = fp16(Q' - hi).
+// A quad of threads per 32-value block of one (query, head) row, 8 values each:
+// q8_0 with ggml's x86 rounding (d = amax/127 over the block, codes =
+// rint(x * 127/amax)), then Q' = code * qd with qd = fp16(d) * scale * log2(e) in
+// fp32, written as fp16 hi = fp16(Q') and lo = fp16(Q' - hi).
 __global__ __launch_bounds__(256) void qprep_kernel(const char *__restrict__ q, int64_t nb1, int64_t nb2,
                                                     int n_q, int H, float qscale, uint16_t *__restrict__ qh,
                                                     uint16_t *__restrict__ ql, uint32_t *__restrict__ dvmax, int hkv,
                                                     bool aligned) {
+    // one thread per 8 values: a quad of lanes owns a 32-value block
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (gid < hkv) dvmax[gid] = 0;  // for kvprep_kernel, launched next
-    if (gid >= (int64_t)n_q * H * kBlocksPerHead) return;
-    const int b = (int)(gid % kBlocksPerHead);
-    const int64_t row = gid / kBlocksPerHead;  // t * H + h
+    if (gid >= (int64_t)n_q * H * kBlocksPerHead * 4) return;  // whole quads: the total is a multiple of 4
+    const int qtr = (int)(gid & 3);
+    const int64_t bid = gid >> 2;
+    const int b = (int)(bid % kBlocksPerHead);
+    const int64_t row = bid / kBlocksPerHead;  // t * H + h
     const int h = (int)(row % H);
     const int64_t t = row / H;
-    const float *x = reinterpret_cast<const float *>(q + t * nb1 + h * nb2) + 32 * b;
-    float v[32];
-    float amax = 0.0f;
+    const float *x = reinterpret_cast<const float *>(q + t * nb1 + h * nb2) + 32 * b + 8 * qtr;
+    float v[8];
     if (aligned) {  // 16-byte aligned rows: vector loads
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 2; ++j) {
             const float4 f = reinterpret_cast<const float4 *>(x)[j];
             v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < 32; ++j) v[j] = x[j];
+        for (int j = 0; j < 8; ++j) v[j] = x[j];
     }
+    float amax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    // the block's amax over the quad (quad_perm [1,0,3,2], then [2,3,0,1])
+    amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xf, 0xf, false)));
+    amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0x4E, 0xf, 0xf, false)));
     const float d = amax / 127.f;
     const float id = amax != 0.0f ? 127.f / amax : 0.0f;
     const float qd = (float)(_Float16)d * qscale;
-    uint16_t oh[32], ol[32];
+    uint16_t oh[8], ol[8];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
+    for (int j = 0; j < 8; ++j) {
         // x opaque: left visible, the compiler may round code * qd to fp16 twice
         // (once from the fp32 product for hi, once from the exact product for the
         // hi it subtracts), and a hi + lo off by one fp16 ulp of hi
-        float x = rintf(v[j] * id) * qd;
-        asm volatile("" : "+v"(x));
-        const _Float16 h = (_Float16)x;
-        const _Float16 l = (_Float16)(x - (float)h);
-        __builtin_memcpy(&oh[j], &h, 2);
-        __builtin_memcpy(&ol[j], &l, 2);
+        float xx = rintf(v[j] * id) * qd;
+        asm volatile("" : "+v"(xx));
+        const _Float16 hh = (_Float16)xx;
+        const _Float16 ll = (_Float16)(xx - (float)hh);
+        __builtin_memcpy(&oh[j], &hh, 2);
+        __builtin_memcpy(&ol[j], &ll, 2);
     }
-    uint4 *h4 = reinterpret_cast<uint4 *>(qh + row * kHeadDim + 32 * b);
-    uint4 *l4 = reinterpret_cast<uint4 *>(ql + row * kHeadDim + 32 * b);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        uint4 a, c;
-        __builtin_memcpy(&a, oh + 8 * j, 16);
-        __builtin_memcpy(&c, ol + 8 * j, 16);
-        h4[j] = a;
-        l4[j] = c;
-    }
+    uint4 a, c;
+    __builtin_memcpy(&a, oh, 16);
+    __builtin_memcpy(&c, ol, 16);
+    *reinterpret_cast<uint4 *>(qh + row * kHeadDim + 32 * b + 8 * qtr) = a;
+    *reinterpret_cast<uint4 *>(ql + row * kHeadDim + 32 * b + 8 * qtr) = c;
 }
 
 // Copies an F16 mask whose rows are unaligned or whose length is not a
@@ -843,7 +844,7 @@ int launch_fa_prefill(const FaArgs &a, hipStream_t s) {
     int prof = profile_start("fa_prefill_prep", s);
     {
         const int64_t nqb = n_q * H * kBlocksPerHead;
-        qprep_kernel<<<dim3((unsigned)((nqb + 255) / 256)), dim3(256), 0, s>>>(
+        qprep_kernel<<<dim3((unsigned)((4 * nqb + 255) / 256)), dim3(256), 0, s>>>(
             (const char *)q.data, (int64_t)q.nb[1], (int64_t)q.nb[2], (int)n_q, (int)H, a.scale * kLog2e, qh, ql,
             dvmax, (int)Hkv, (uintptr_t)q.data % 16 == 0 && q.nb[1] % 16 == 0 && q.nb[2] % 16 == 0);
         kvprep_kernel<<<dim3((unsigned)(pl.kv_tiles / 2), (unsigned)Hkv), dim3(256), 0, s>>>(
