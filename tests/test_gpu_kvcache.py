@@ -96,6 +96,34 @@ def test_prefill_then_decode_through_kv_cache(sqa, orc, dev):
     assert s0 == 515 and kv.n_used == 516
 
 
+def test_mtp_head_cache_beside_the_trunk(sqa, orc, dev):
+    """The MTP head runs the same full-attention layer over a KV cache of its own
+    (reference: src/model/mtp.rs:78 KvCache::new(.., 1 layer, ..) and :186-199
+    build_attn_layer on st.kv): a catch-up over the committed tokens (n >= 1),
+    then one draft position at a time (n = 1), interleaved with the trunk's
+    decode and verify steps and its rewind after a rejected draft. Both caches
+    go through the same library calls; every attention output is checked
+    against the oracle on a host copy of its own cache."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(193)
+    trunk = sqa.KvCache(N_LAYERS, D, HKV, CAP, device=dev)
+    mtp = sqa.KvCache(1, D, HKV, 1000, device=dev)
+    for kv in (trunk, mtp):
+        for t in kv.k + kv.v:
+            t.fill_(0xFF)
+        kv.zero_caches()
+    _step(sqa, trunk, orc, gen, dev, 16, "trunk prefill 16")
+    _step(sqa, mtp, orc, gen, dev, 16, "mtp catch-up 16", n_layers=1)
+    for i in range(3):
+        _step(sqa, mtp, orc, gen, dev, 1, f"mtp draft {i}", n_layers=1)
+        _step(sqa, trunk, orc, gen, dev, 2, f"trunk verify {i}")
+        if i % 2 == 0:  # draft rejected: both caches drop it
+            trunk.rewind_to(trunk.n_used - 1)
+            mtp.rewind_to(mtp.n_used - 1)
+            _step(sqa, mtp, orc, gen, dev, 1, f"mtp catch-up {i}", n_layers=1)
+    assert trunk.n_used == 16 + 2 * 3 - 2 and mtp.n_used == 16 + 3
+
+
 def test_graph_replayed_decode_step_matches_oracle(sqa, orc, dev):
     gen = torch.Generator(device=dev)
     gen.manual_seed(779)
