@@ -638,6 +638,13 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         if (n_tiles > 0) issue_k(0);
         if (n_tiles > 1) issue_k(1);
         if (n_tiles > 0) issue_v(0);
+        if (!TWO) {
+            // rows 8-15 of both P buffers (never written with 8 rows) hold zeros: the
+            // residual operand of the lanes that carry hi parts (see the PV below)
+            const int zi = vw * 64 + lane;  // 256 lanes x 4 fp16 = 2 buffers x 8 rows x 64 hi
+            *reinterpret_cast<half4 *>(pbuf + ((zi >> 7) * 16 + 8 + ((zi >> 4) & 7)) * kPRow + 4 * (zi & 15)) =
+                half4{0, 0, 0, 0};
+        }
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // Q operands published
         const int dq = wq;  // dims 64dq..64dq+63: blocks 2dq, 2dq+1
         // B operand straight from the nibbles: a nibble in the low bits of an fp16
@@ -710,13 +717,21 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             const uint4 fl = *reinterpret_cast<const uint4 *>(fbuf + pb * 4);
 
             // -- P rows (k-slot order), read first: their latency runs under the
-            // d_v compaction below
-            const _Float16 *prow = pbuf + (pb * 16 + ra) * kPRow + 8 * g;
-            half8 pa[2], pl[2];  // P hi and lo of tile halves 0, 1
-            pa[0] = *reinterpret_cast<const half8 *>(prow);
-            pa[1] = *reinterpret_cast<const half8 *>(prow + 32);
-            pl[0] = *reinterpret_cast<const half8 *>(prow + 64);
-            pl[1] = *reinterpret_cast<const half8 *>(prow + 96);
+            // d_v compaction below. 16 rows: pa, pl = hi and lo of row n. Up to 8 rows:
+            // A row n < 8 carries the hi part of P d_v of row n and A row n + 8 its lo
+            // part (C rows r and r + 8 are summed at the end), so one set of MFMAs
+            // serves both: pa = the P part the lane multiplies (hi of row n, lo of row
+            // n - 8), pl = the hi part whose rounding residual the lane adds (zero row
+            // n + 8, hi of row n - 8).
+            half8 pa[2], pl[2];  // tile halves 0, 1
+            {
+                const _Float16 *arow = pbuf + (pb * 16 + ra) * kPRow + 8 * g + (TWO || n < 8 ? 0 : 64);
+                const _Float16 *lrow = TWO ? arow + 64 : pbuf + (pb * 16 + (n ^ 8)) * kPRow + 8 * g;
+                pa[0] = *reinterpret_cast<const half8 *>(arow);
+                pa[1] = *reinterpret_cast<const half8 *>(arow + 32);
+                pl[0] = *reinterpret_cast<const half8 *>(lrow);
+                pl[1] = *reinterpret_cast<const half8 *>(lrow + 32);
+            }
 
             // -- d_v of the slice's two blocks for all 64 keys, in B k-slot order --
             // A key no row sees (masked, past the range or past the cache end) gets
@@ -781,14 +796,20 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
 #pragma unroll
                 for (int w = 0; w < 4; ++w) mw[w] = mr[16 * w + ra];
                 const float mna = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+                const _Float16 *prow = pbuf + (pb * 16 + ra) * kPRow + 8 * g;  // hi | lo of row ra
 #pragma unroll
-                for (int h = 0; h < 2; ++h)
+                for (int h = 0; h < 2; ++h) {
+                    const half8 ph = *reinterpret_cast<const half8 *>(prow + 32 * h);
+                    const half8 plo = *reinterpret_cast<const half8 *>(prow + 64 + 32 * h);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        const float xv = ((float)pa[h][e] + (float)pl[h][e]) * exp2_or_zero(mw[2 * h + (g >> 1)], mna);
-                        pa[h][e] = (_Float16)xv;
-                        pl[h][e] = (_Float16)(xv - (float)pa[h][e]);
+                        const float xv = ((float)ph[e] + (float)plo[e]) * exp2_or_zero(mw[2 * h + (g >> 1)], mna);
+                        const _Float16 hi = (_Float16)xv;
+                        const _Float16 lo = (_Float16)(xv - (float)hi);
+                        pa[h][e] = TWO || n < 8 ? hi : lo;
+                        pl[h][e] = TWO ? lo : (n < 8 ? (_Float16)0 : hi);
                     }
+                }
             }
 
             // -- O += P V over the two halves of the tile and the slice's blocks ---
@@ -821,9 +842,6 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                     const uint4 dv4 = *reinterpret_cast<const uint4 *>(dv_comp + ((bl * 2 + h) * 4 + g) * 16);
                     half8 dv8;
                     __builtin_memcpy(&dv8, &dv4, 16);
-                    const half8 ah = pa[h] * dv8;
-                    const half8 ar = __builtin_elementwise_fma(pa[h], dv8, -ah);
-                    const half8 al = __builtin_elementwise_fma(pl[h], dv8, ar);
                     uint32_t wlo[4], whi[4];
 #pragma unroll
                     for (int m = 0; m < 4; ++m) {
@@ -833,12 +851,26 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                     half8 blo, bhi;
                     __builtin_memcpy(&blo, wlo, 16);
                     __builtin_memcpy(&bhi, whi, 16);
-                    acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, blo, acc[2 * bl], 0, 0, 0);
-                    acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bhi, acc[2 * bl + 1], 0, 0, 0);
-                    cor[bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ones, cor[bl], 0, 0, 0);
-                    acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, blo, acc[2 * bl], 0, 0, 0);
-                    acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bhi, acc[2 * bl + 1], 0, 0, 0);
-                    cor[bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, ones, cor[bl], 0, 0, 0);
+                    if (TWO) {
+                        const half8 ah = pa[h] * dv8;
+                        const half8 ar = __builtin_elementwise_fma(pa[h], dv8, -ah);
+                        const half8 al = __builtin_elementwise_fma(pl[h], dv8, ar);
+                        acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, blo, acc[2 * bl], 0, 0, 0);
+                        acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bhi, acc[2 * bl + 1], 0, 0, 0);
+                        cor[bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, ones, cor[bl], 0, 0, 0);
+                        acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, blo, acc[2 * bl], 0, 0, 0);
+                        acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bhi, acc[2 * bl + 1], 0, 0, 0);
+                        cor[bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, ones, cor[bl], 0, 0, 0);
+                    } else {
+                        // hi lanes: pl = 0, so a = round(pa d_v); lo lanes: a = pl_lo d_v plus the
+                        // exact residual of the hi part, rounded once
+                        const half8 th = pl[h] * dv8;
+                        const half8 tr = __builtin_elementwise_fma(pl[h], dv8, -th);
+                        const half8 a = __builtin_elementwise_fma(pa[h], dv8, tr);
+                        acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, blo, acc[2 * bl], 0, 0, 0);
+                        acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bhi, acc[2 * bl + 1], 0, 0, 0);
+                        cor[bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ones, cor[bl], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -846,10 +878,19 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         // ---------------- this split's partial O (un-normalised) -----------------
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // pairs the statistics barrier
         const float o_scale = __builtin_amdgcn_ldexpf(1.0f, -e_dv);
+        if (!TWO) {  // C row r + 8 (lanes g + 2 = lane ^ 32) holds the lo part of row r
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int T = 0; T < 4; ++T) acc[T][i] = xsum32(acc[T][i]);
+                cor[0][i] = xsum32(cor[0][i]);
+                cor[1][i] = xsum32(cor[1][i]);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 4 * g + i;
-            if (row < p.rows) {
+            if (row < p.rows && (TWO || g < 2)) {
                 const int tq = row / p.G, hq = kvh * p.G + row % p.G;
                 float *dst = p.part_acc + ((int64_t)split * rows_total + (int64_t)tq * p.H + hq) * 256 + 64 * dq + n;
 #pragma unroll
