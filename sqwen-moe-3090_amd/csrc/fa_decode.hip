@@ -198,6 +198,14 @@ __device__ __forceinline__ int xsum16(int x) {
     const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)x, (uint32_t)x, false, false);
     return (int)(r[0] + r[1]);
 }
+__device__ __forceinline__ uint32_t or16(uint32_t x) {  // x | x of lane ^ 16
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return r[0] | r[1];
+}
+__device__ __forceinline__ uint32_t or32(uint32_t x) {  // x | x of lane ^ 32
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return r[0] | r[1];
+}
 // x of lane ^ 32: lanes 0-31 find it in the swapped source, lanes 32-63 in the
 // swapped destination
 __device__ __forceinline__ int xother32(int x) {
@@ -409,6 +417,16 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         const int dk_src = lds_byte<false>(key0 + 4 * dk_gg + 2 * dk_hh, 18 * dk_blk);
         const int dk_dst = (dk_blk * 16 + 4 * dk_gg + 2 * dk_hh) * 2;
 
+        // first tile holding keys past the range end (k1) or past a causal limit
+        // (key > q_pos0 for the first position): tile t ends at key k0 + 64t + 63
+        int t_tail = (int)((k1 - k0) / kTileKeys);
+        if (p.q_pos0 >= 0) {
+            const int64_t x = p.q_pos0 - k0 - (kTileKeys - 1);  // tail when 64t > x
+            if (x < 0)
+                t_tail = 0;
+            else if (x / kTileKeys < t_tail)
+                t_tail = (int)(x / kTileKeys) + 1;
+        }
         float m_ref = -INFINITY;   // base-2 reference max of row my_r (common to the workgroup)
         float m_used = -INFINITY;  // reference this wavefront used for the last tile's P
         float l_acc = 0.0f;        // this lane's share of the row's sum, relative to m_ref
@@ -438,7 +456,7 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             const int st = t % kKStages;
             const uint8_t *sK = smem + st * kTensorBytes;
             // a tile holding keys past the range end or past a causal limit
-            const bool tail = kt + kTileKeys > k1 || (p.q_pos0 >= 0 && kt + kTileKeys - 1 > p.q_pos0);
+            const bool tail = t >= t_tail;
 
             // A row r of QK is key key0 + r, so lane group g holds keys key0 + 4g + i.
             // -- compact d_k of those keys, [block][4g + i] ------------------------
@@ -524,10 +542,11 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                 mu = fmaxf(m_ref, mt);
             }
             m_used = mu;
-            const float mb = mu == -INFINITY ? 0.0f : mu;
+            // the reference plus the P shift: exact while |mu| < 2^21
+            const float mb = (mu == -INFINITY ? 0.0f : mu) + kPShift;
             float pv[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_exp2f(s[i] - mb - kPShift);
+            for (int i = 0; i < 4; ++i) pv[i] = __builtin_amdgcn_exp2f(s[i] - mb);
             l_prev = (pv[0] + pv[1]) + (pv[2] + pv[3]);
             const int buf = t & 1;
             if (row_writer) {
@@ -549,15 +568,18 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                 *reinterpret_cast<half4 *>(prow + 64) = pl;
                 if (g == 0) mbuf[(buf * 4 + wq) * 16 + my_r] = mu;
             }
-            // keys of this wavefront that some row sees: bit 4g + i of the 16
-            uint32_t alive16 = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint64_t b = __ballot(pv[i] != 0.0f);  // bit 16g + n: row n, key 4g + i
-#pragma unroll
-                for (int gg = 0; gg < 4; ++gg) alive16 |= ((b >> (16 * gg)) & 0xFFFFu) ? 1u << (4 * gg + i) : 0u;
-            }
-            if (lane == 0) fbuf[buf * 4 + wq] = (need ? 1u : 0u) | (alive16 << 16);
+            // keys of this wavefront that some row sees: bit 4g + i of the 16. P >= 0
+            // (or NaN), so P != 0 is a nonzero bit pattern; the 16 lanes of group g
+            // (one DPP row) OR their nibbles, the four groups then OR theirs.
+            uint32_t alive = min(__float_as_uint(pv[0]), 1u) | (min(__float_as_uint(pv[1]), 1u) << 1) |
+                             (min(__float_as_uint(pv[2]), 1u) << 2) | (min(__float_as_uint(pv[3]), 1u) << 3);
+            alive |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)alive, 0x121, 0xf, 0xf, false);  // row_ror:1
+            alive |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)alive, 0x122, 0xf, 0xf, false);  // row_ror:2
+            alive |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)alive, 0x124, 0xf, 0xf, false);  // row_ror:4
+            alive |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)alive, 0x128, 0xf, 0xf, false);  // row_ror:8
+            alive = or16(alive << (4 * g));
+            alive = or32(alive);
+            if (lane == 0) fbuf[buf * 4 + wq] = (need ? 1u : 0u) | (alive << 16);
         }
 
         // ---------------- this split's softmax statistics ------------------------
@@ -595,31 +617,53 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         const int per_k = nk + (mask_dma ? 1 : 0);  // DMA instructions per K tile (wave-uniform)
         const int per_v = nv;
 
-        // keys past the cache end re-read its last row (they are masked off)
+        // keys past the cache end re-read its last row (they are masked off); mask
+        // segments past the readable length re-read its last 16 bytes
         auto lim_of = [&](int64_t kt) -> uint32_t {
             return p.n_kv - kt >= kTileKeys ? 0xFFFFFFFFu : (uint32_t)((p.n_kv - kt) * kCacheRow - 16);
         };
+        auto mlim_of = [&](int64_t kt) -> uint32_t {
+            return p.mask_len - kt >= kTileKeys + 8 ? 0xFFFFFFFFu : (uint32_t)((p.mask_len - 8 - kt) * 2);
+        };
+        // Tiles below t_fast need neither limit: tile t starts at key k0 + 64t, and
+        // lim_of / mlim_of are unlimited while 64t <= n_kv - k0 - 64 and
+        // 64t <= mask_len - k0 - 72.
+        int t_fast = (int)min((int64_t)n_tiles, (p.n_kv - k0) / kTileKeys);
+        if (mask_dma) {
+            const int64_t y = p.mask_len - k0 - (kTileKeys + 8);
+            t_fast = y < 0 ? 0 : (int)min((int64_t)t_fast, y / kTileKeys + 1);
+        }
+        const uint8_t *kb0 = p.k + k0 * kCacheRow;
+        const uint8_t *vb0 = p.v + k0 * kCacheRow;
+        const char *mb0 = p.mask ? p.mask + k0 * 2 : nullptr;
+        const bool mask_lane = mask_dma && mrow_l < p.n_q;
         auto issue_k = [&](int t) {
-            const int64_t kt = k0 + (int64_t)t * kTileKeys;
-            const uint32_t lim = lim_of(kt);
-            const uint8_t *kb = p.k + kt * kCacheRow;
+            const uint8_t *kb = kb0 + (int64_t)t * (kTileKeys * kCacheRow);
             const int st = t % kKStages;
             const uint32_t kbase = lds0 + st * kTensorBytes;
+            const uint32_t mdst = lds0 + kOffMask + st * kMaskStageBytes;
+            if (t < t_fast) {
 #pragma unroll
-            for (int r = 0; r < 3; ++r)
-                if (r < nk) dma16(koff[r] < lim ? koff[r] : lim, kb, kbase + 1024u * (vw + 4 * r));
-            if (mask_dma) {
-                const uint32_t mlim =
-                    p.mask_len - kt >= kTileKeys + 8 ? 0xFFFFFFFFu : (uint32_t)((p.mask_len - 8 - kt) * 2);
-                const uint32_t mo = moff - 16 * (lane & 7) + ((16u * (lane & 7)) < mlim ? 16u * (lane & 7) : mlim);
-                if (mrow_l < p.n_q) dma16(mo, p.mask + kt * 2, lds0 + kOffMask + st * kMaskStageBytes);
+                for (int r = 0; r < 3; ++r)
+                    if (r < nk) dma16(koff[r], kb, kbase + 1024u * (vw + 4 * r));
+                if (mask_lane) dma16(moff, mb0 + (int64_t)t * (kTileKeys * 2), mdst);
+            } else {
+                const int64_t kt = k0 + (int64_t)t * kTileKeys;
+                const uint32_t lim = lim_of(kt);
+#pragma unroll
+                for (int r = 0; r < 3; ++r)
+                    if (r < nk) dma16(koff[r] < lim ? koff[r] : lim, kb, kbase + 1024u * (vw + 4 * r));
+                if (mask_dma) {
+                    const uint32_t mlim = mlim_of(kt);
+                    const uint32_t mo = moff - 16 * (lane & 7) + ((16u * (lane & 7)) < mlim ? 16u * (lane & 7) : mlim);
+                    if (mrow_l < p.n_q) dma16(mo, mb0 + (int64_t)t * (kTileKeys * 2), mdst);
+                }
             }
         };
         auto issue_v = [&](int t) {
-            const int64_t kt = k0 + (int64_t)t * kTileKeys;
-            const uint32_t lim = lim_of(kt);
-            const uint8_t *vb = p.v + kt * kCacheRow;
+            const uint8_t *vb = vb0 + (int64_t)t * (kTileKeys * kCacheRow);
             const uint32_t vbase = lds0 + kOffV + (t % kVStages) * kTensorBytes;
+            const uint32_t lim = t < t_fast ? 0xFFFFFFFFu : lim_of(k0 + (int64_t)t * kTileKeys);
 #pragma unroll
             for (int r = 0; r < 3; ++r)
                 if (r < nv) dma16(voff[r] < lim ? voff[r] : lim, vb, vbase + 1024u * (((vw + 2) & 3) + 4 * r));
