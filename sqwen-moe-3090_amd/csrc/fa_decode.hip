@@ -213,6 +213,21 @@ __device__ __forceinline__ int xother32(int x) {
     return (int)((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
+// a * b - c in packed fp16, the negation as an operand modifier (written as
+// -c in C, the backend lowers the negation of the first pair as three VALU)
+__device__ __forceinline__ half8 fma_minus(half8 a, half8 b, half8 c) {
+    uint32_t x[4], y[4], z[4], r[4];
+    __builtin_memcpy(x, &a, 16);
+    __builtin_memcpy(y, &b, 16);
+    __builtin_memcpy(z, &c, 16);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+        asm("v_pk_fma_f16 %0, %1, %2, %3 neg_lo:[0,0,1] neg_hi:[0,0,1]" : "=v"(r[m]) : "v"(x[m]), "v"(y[m]), "v"(z[m]));
+    half8 o;
+    __builtin_memcpy(&o, r, 16);
+    return o;
+}
+
 __device__ __forceinline__ float exp2_or_zero(float a, float b) {  // 2^(a-b), 0 when a = -inf
     return a == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(a - b);
 }
@@ -909,7 +924,7 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                         // hi lanes: pl = 0, so a = round(pa d_v); lo lanes: a = pl_lo d_v plus the
                         // exact residual of the hi part, rounded once
                         const half8 th = pl[h] * dv8;
-                        const half8 tr = __builtin_elementwise_fma(pl[h], dv8, -th);
+                        const half8 tr = fma_minus(pl[h], dv8, th);
                         const half8 a = __builtin_elementwise_fma(pa[h], dv8, tr);
                         acc[2 * bl] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, blo, acc[2 * bl], 0, 0, 0);
                         acc[2 * bl + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bhi, acc[2 * bl + 1], 0, 0, 0);
