@@ -293,7 +293,10 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
     const int n = lane & 15;
     const bool score = wave < kScoreWaves;
     const int wq = wave & 3;  // score: 16-key quarter of every tile; value: 64-dim slice
-    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+    // LDS byte address of smem, computed once: the cast carries a null check the
+    // compiler would otherwise repeat at every use
+    uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+    asm volatile("" : "+s"(lds0));
     constexpr int kRowMask = TWO ? 15 : 7;  // rows 8-15 mirror rows 0-7 when only 8 exist
 
     // ---------------- split and KV head of this workgroup ---------------------
@@ -446,6 +449,11 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         float m_used = -INFINITY;  // reference this wavefront used for the last tile's P
         float l_acc = 0.0f;        // this lane's share of the row's sum, relative to m_ref
         float l_prev = 0.0f;       // the last tile's share, relative to m_used
+        // K stage of the tile (t mod kKStages, carried through the loop: LDS
+        // addresses are then one add of a wave-uniform offset) and this lane's P
+        // row in tile buffer 0
+        int st = 0;
+        _Float16 *const prow0 = pbuf + my_r * kPRow + p_col;
 
         for (int tt = 0; tt <= n_tiles; ++tt) {
             // the tile index is wave-uniform; with 16 rows the compiler loses track of that
@@ -468,7 +476,6 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             if (t == n_tiles) break;
 
             const int64_t kt = k0 + (int64_t)t * kTileKeys;
-            const int st = t % kKStages;
             const uint8_t *sK = smem + st * kTensorBytes;
             // a tile holding keys past the range end or past a causal limit
             const bool tail = t >= t_tail;
@@ -578,7 +585,7 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                         asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[0,0,0] op_sel_hi:[0,0,1]" : "=v"(r[i]) : "v"(pv[i]), "v"(hw[i >> 1]));
                 }
                 pl = half4{(_Float16)r[0], (_Float16)r[1], (_Float16)r[2], (_Float16)r[3]};
-                _Float16 *prow = pbuf + (buf * 16 + my_r) * kPRow + p_col;
+                _Float16 *prow = prow0 + buf * (16 * kPRow);
                 *reinterpret_cast<half4 *>(prow) = ph;
                 *reinterpret_cast<half4 *>(prow + 64) = pl;
                 if (g == 0) mbuf[(buf * 4 + wq) * 16 + my_r] = mu;
@@ -595,6 +602,7 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             alive = or16(alive << (4 * g));
             alive = or32(alive);
             if (lane == 0) fbuf[buf * 4 + wq] = (need ? 1u : 0u) | (alive << 16);
+            st = st == kKStages - 1 ? 0 : st + 1;
         }
 
         // ---------------- this split's softmax statistics ------------------------
@@ -652,9 +660,8 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         const uint8_t *vb0 = p.v + k0 * kCacheRow;
         const char *mb0 = p.mask ? p.mask + k0 * 2 : nullptr;
         const bool mask_lane = mask_dma && mrow_l < p.n_q;
-        auto issue_k = [&](int t) {
+        auto issue_k = [&](int t, int st) {  // st = t mod kKStages
             const uint8_t *kb = kb0 + (int64_t)t * (kTileKeys * kCacheRow);
-            const int st = t % kKStages;
             const uint32_t kbase = lds0 + st * kTensorBytes;
             const uint32_t mdst = lds0 + kOffMask + st * kMaskStageBytes;
             if (t < t_fast) {
@@ -675,9 +682,9 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                 }
             }
         };
-        auto issue_v = [&](int t) {
+        auto issue_v = [&](int t, int st) {  // st = t mod kVStages
             const uint8_t *vb = vb0 + (int64_t)t * (kTileKeys * kCacheRow);
-            const uint32_t vbase = lds0 + kOffV + (t % kVStages) * kTensorBytes;
+            const uint32_t vbase = lds0 + kOffV + st * kTensorBytes;
             const uint32_t lim = t < t_fast ? 0xFFFFFFFFu : lim_of(k0 + (int64_t)t * kTileKeys);
 #pragma unroll
             for (int r = 0; r < 3; ++r)
@@ -694,9 +701,10 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
 
         // ---------------- K 0-1 and V 0 ------------------------------------------
         // (V stages 1-2 hold the Q operands until the loop's first barrier)
-        if (n_tiles > 0) issue_k(0);
-        if (n_tiles > 1) issue_k(1);
-        if (n_tiles > 0) issue_v(0);
+        static_assert(kKStages == 3 && kVStages == 3, "the stage counter below");
+        if (n_tiles > 0) issue_k(0, 0);
+        if (n_tiles > 1) issue_k(1, 1);
+        if (n_tiles > 0) issue_v(0, 0);
         if (!TWO) {
             // rows 8-15 of both P buffers (never written with 8 rows) hold zeros: the
             // residual operand of the lanes that carry hi parts (see the PV below)
@@ -759,17 +767,23 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         };
         set_dv_scale(kMaxDvExp);
         float m_acc[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // reference max of rows 4g+i
+        // P rows of this lane in tile buffer 0 (see the PV below)
+        const _Float16 *const arow0 = pbuf + ra * kPRow + 8 * g + (TWO || n < 8 ? 0 : 64);
+        const _Float16 *const lrow0 = TWO ? arow0 + 64 : pbuf + (n ^ 8) * kPRow + 8 * g;
 
+        int c = 0;  // t mod 3, carried through the loop (3 K and 3 V stages)
         for (int tt = 0; tt <= n_tiles; ++tt) {
             const int t = TWO ? __builtin_amdgcn_readfirstlane(tt) : tt;  // wave-uniform tile index
+            const int c1 = c == 2 ? 0 : c + 1, c2 = c == 0 ? 2 : c - 1;  // (t + 1) mod 3, (t + 2) mod 3
             wait_vm_barrier(younger_than_needed(t));
-            if (t + 2 < n_tiles) issue_k(t + 2);
-            if (t + 1 < n_tiles) issue_v(t + 1);
+            if (t + 2 < n_tiles) issue_k(t + 2, c2);
+            if (t + 1 < n_tiles) issue_v(t + 1, c1);
+            c = c1;
             if (t == 0) continue;
 
             const int tv = t - 1;  // PV of the tile whose P the score wavefronts wrote last
             const int pb = tv & 1;
-            const uint32_t sv_off = (uint32_t)(kOffV + (tv % kVStages) * kTensorBytes);  // wave-uniform
+            const uint32_t sv_off = (uint32_t)(kOffV + c2 * kTensorBytes);  // stage of V(t - 1), wave-uniform
 
             // flags of the score wavefronts: bit 0 = maximum moved, bits 16-31 = their
             // 16 keys that some row of the call can see (P != 0)
@@ -784,8 +798,8 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             // n + 8, hi of row n - 8).
             half8 pa[2], pl[2];  // tile halves 0, 1
             {
-                const _Float16 *arow = pbuf + (pb * 16 + ra) * kPRow + 8 * g + (TWO || n < 8 ? 0 : 64);
-                const _Float16 *lrow = TWO ? arow + 64 : pbuf + (pb * 16 + (n ^ 8)) * kPRow + 8 * g;
+                const _Float16 *arow = arow0 + pb * (16 * kPRow);
+                const _Float16 *lrow = lrow0 + pb * (16 * kPRow);
                 pa[0] = *reinterpret_cast<const half8 *>(arow);
                 pa[1] = *reinterpret_cast<const half8 *>(arow + 32);
                 pl[0] = *reinterpret_cast<const half8 *>(lrow);
@@ -889,7 +903,6 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
 #pragma unroll
                     for (int mp = 0; mp < 2; ++mp) {
                         uint32_t va = lds0 + sv_off + vlane[bl] + (uint32_t)((32 * h + 4 * mp) * kLdsRow);
-                        asm volatile("" : "+v"(va));  // opaque: no induction variable per address
                         const lds_u32 *r0 = reinterpret_cast<const lds_u32 *>((uintptr_t)va);
 #pragma unroll
                         for (int m2 = 0; m2 < 2; ++m2)
