@@ -545,7 +545,16 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj) s[rg][jj] = sa[rg][jj >> 2][jj & 3];
             // ---- mask / causal / ragged tail ----------------------------------------
+            // a block of the mask that is +0 for all of this wave's rows and keys (every
+            // fully visible tile of a causal mask) changes no logit: skip it
+            bool mask_live = false;
             if (p.mask) {
+                uint32_t any = 0;
+#pragma unroll
+                for (int rg = 0; rg < kRG; ++rg) any |= mrow[rg].x | mrow[rg].y | mrow[rg].z | mrow[rg].w;
+                mask_live = __any(any != 0u);
+            }
+            if (mask_live) {
 #pragma unroll
                 for (int rg = 0; rg < kRG; ++rg) {
                     const uint32_t mw[4] = {mrow[rg].x, mrow[rg].y, mrow[rg].z, mrow[rg].w};
