@@ -609,9 +609,19 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                 // P as an fp16 hi + lo pair (22 bits): the value waves form P d_v from it
                 half8 ph, pl;
 #pragma unroll
+                for (int jj = 0; jj < 8; ++jj) ph[jj] = (_Float16)pf[jj];
+                // the exact residual p - hi, with hi read from its packed fp16 half by
+                // v_fma_mix (no conversion of hi back to fp32)
+                uint32_t hw[4];
+                __builtin_memcpy(hw, &ph, 16);
+#pragma unroll
                 for (int jj = 0; jj < 8; ++jj) {
-                    ph[jj] = (_Float16)pf[jj];
-                    pl[jj] = (_Float16)(pf[jj] - (float)ph[jj]);
+                    float r;
+                    if (jj & 1)
+                        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "=v"(r) : "v"(pf[jj]), "v"(hw[jj >> 1]));
+                    else
+                        asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[0,0,0] op_sel_hi:[0,0,1]" : "=v"(r) : "v"(pf[jj]), "v"(hw[jj >> 1]));
+                    pl[jj] = (_Float16)r;
                 }
                 *reinterpret_cast<half8 *>(pb + rg * 2048) = ph;
                 *reinterpret_cast<half8 *>(pb + rg * 2048 + 1024) = pl;
