@@ -455,6 +455,12 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
         half8 bqh[kRG][8], bql[kRG][8];
         int my_pos[kRG], m_off[kRG];
         float m_run[kRG], l_part[kRG];
+        // The logits are accumulated relative to the row's P reference mref =
+        // (m_run, or 0 before the first visible key) - ep: s' = s - mref, so that
+        // P = 2^s' needs no subtraction, and the lazy-maximum test s > m_run +
+        // kSlack reads s' > lim_s (kSlack + ep, or -inf before the first visible
+        // key). Both change only when the maximum moves.
+        float mref[kRG], lim_s[kRG];
 #pragma unroll
         for (int rg = 0; rg < kRG; ++rg) {
             const int r = 32 * w + 16 * rg + n;
@@ -476,6 +482,8 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             m_off[rg] = kLdsMask + 64 * pl + 16 * (g ^ ((pl >> 1) & 3));
             m_run[rg] = -INFINITY;
             l_part[rg] = 0.0f;
+            mref[rg] = -(float)ep;
+            lim_s[rg] = -INFINITY;
         }
         // K operand of key row 16kg + n, dims 32b + 8g..+7: chunk (4b + g) ^ (n & 7),
         // halves swapped when n & 8; the XOR touches bit 2 of 4b + g, so even and odd
@@ -516,7 +524,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             // ---- S^T: sa[rg][kg][i] = S[key kt + 8g + 4kg + i][row n of group rg] ----
             floatx4 sa[kRG][2];
 #pragma unroll
-            for (int rg = 0; rg < kRG; ++rg) sa[rg][0] = sa[rg][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int rg = 0; rg < kRG; ++rg) sa[rg][0] = sa[rg][1] = -mref[rg];
             // d_k of the lane's four C rows 16kg + 4g + i, block b: 8 bytes at
             // Dk[b][16kg + 4g]
             const uint8_t *dkb = smem + (t & 1) * kKStage + kOffDk + 8 * g;
@@ -585,24 +593,29 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                 // than kSlack, so P <= 2^kSlack and most tiles need no rescale of O
                 float alpha = 1.0f;
                 bool over = false;
-                const float lim = m_run[rg] + kSlack;
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) over |= s[rg][jj] > lim;
+                for (int jj = 0; jj < 8; ++jj) over |= s[rg][jj] > lim_s[rg];
                 if (__any(over)) {
                     float mt = fmaxf(fmaxf(fmaxf(s[rg][0], s[rg][1]), fmaxf(s[rg][2], s[rg][3])),
                                      fmaxf(fmaxf(s[rg][4], s[rg][5]), fmaxf(s[rg][6], s[rg][7])));
                     mt = xmax16(mt);
                     mt = xmax32(mt);
-                    const float m_new = fmaxf(m_run[rg], mt);
+                    const float m_new = fmaxf(m_run[rg], mt + mref[rg]);
                     alpha = m_run[rg] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[rg] - m_new);
                     l_part[rg] *= alpha;
                     m_run[rg] = m_new;
+                    // onto the new reference: s - mref_new = s' + (mref - mref_new)
+                    const float mref_new = (m_new == -INFINITY ? 0.0f : m_new) - (float)ep;
+                    const float d = mref[rg] - mref_new;
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) s[rg][jj] += d;
+                    mref[rg] = mref_new;
+                    lim_s[rg] = m_new == -INFINITY ? -INFINITY : kSlack + (float)ep;
                 }
-                const float mref = (m_run[rg] == -INFINITY ? 0.0f : m_run[rg]) - (float)ep;
                 float pf[8], psum = 0.0f;
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj) {
-                    pf[jj] = __builtin_amdgcn_exp2f(s[rg][jj] - mref);
+                    pf[jj] = __builtin_amdgcn_exp2f(s[rg][jj]);
                     psum += pf[jj];
                 }
                 l_part[rg] += psum;
