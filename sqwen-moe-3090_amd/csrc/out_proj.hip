@@ -635,12 +635,15 @@ __global__ __launch_bounds__(64 * kG2Waves) void op_gemm2_kernel(Gemm2Params p) 
 // Decode and verify (M <= 4 tokens, MT = 1, 2 or 4 slots): one workgroup of 256
 // threads takes 8 rows of W; thread (row, l32) takes half h = l32 & 1 (code
 // groups 2h, 2h+1) of super-blocks l32 / 2, l32 / 2 + 16, ... of its row, so a
-// row's bytes are read by 32 consecutive threads. Each code is dequantized in
-// fp32 and the thread accumulates sum(code * xg) and sum(xg) per sub-block:
-// out += d*scale * sum(code * xg) - dmin*min * sum(xg). The gated activations
-// and their sub-block sums are built in LDS by the workgroup itself (no
-// separate pass), while the thread's first weights are already in flight.
-template <int MT>
+// row's bytes are read by 32 consecutive threads. The thread accumulates
+// sum(code * xg) and sum(xg) per sub-block: out += d*scale * sum(code * xg) -
+// dmin*min * sum(xg). Codes enter as fp16 subnormals (code * 2^-24, two per
+// v_and) into v_fma_mix with the fp32 activations, so every product is exact
+// and the 2^24 goes into the scale. The gated activations and their sub-block
+// sums are built in LDS by the workgroup itself (no separate pass), while the
+// thread's first weights are already in flight. VEC: x (and gate) rows are
+// 16-byte aligned and read four floats at a time.
+template <int MT, bool VEC>
 __global__ __launch_bounds__(256) void op_gemv_kernel(const uint8_t *__restrict__ w, int64_t w_nb1,
                                                       const char *__restrict__ x, int64_t x_nb1,
                                                       const char *__restrict__ gate, int64_t g_nb1, int K, int N,
@@ -664,43 +667,74 @@ __global__ __launch_bounds__(256) void op_gemv_kernel(const uint8_t *__restrict_
         for (int c = 0; c < 4; ++c) qb[c] = blk[1 + 4 * hj + c];
     };
     if ((l32 >> 1) < nsb) load_w(l32 >> 1);  // in flight while the activations load
-    // 16 values per thread per round, all loads of a round issued before any use
-    for (int i0 = 0; i0 < MT * K; i0 += 256 * 16) {
-        float v[16], gv[16];
+    auto gated = [&](float v, float g) { return gate ? v * (1.0f / (1.0f + expf(-g))) : v; };
+    if (VEC) {
+        // 16 values per thread per round as four float4, all loads of a round
+        // issued before any use (K is a multiple of 256: a float4 stays in one token row)
+        for (int i0 = 0; i0 < MT * K; i0 += 256 * 16) {
+            float4 v[4], gv[4];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int i = i0 + 256 * u + tid;
-            const int t = i / K, k = i - t * K;
-            const bool ok = i < MT * K && t < M;
-            v[u] = ok ? reinterpret_cast<const float *>(x + t * x_nb1)[k] : 0.0f;
-            gv[u] = ok && gate ? reinterpret_cast<const float *>(gate + t * g_nb1)[k] : 0.0f;
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + 4 * (256 * u + tid);
+                const int t = i / K, k = i - t * K;
+                const bool ok = i < MT * K && t < M;
+                v[u] = gv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (ok) {
+                    v[u] = *reinterpret_cast<const float4 *>(x + t * x_nb1 + 4 * (int64_t)k);
+                    if (gate) gv[u] = *reinterpret_cast<const float4 *>(gate + t * g_nb1 + 4 * (int64_t)k);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + 4 * (256 * u + tid);
+                const int t = i / K, k = i - t * K;
+                if (i < MT * K)
+                    *reinterpret_cast<float4 *>(xs + t * tstride + (k >> 8) * kGemvSbStride + (k & 255)) =
+                        make_float4(gated(v[u].x, gv[u].x), gated(v[u].y, gv[u].y), gated(v[u].z, gv[u].z),
+                                    gated(v[u].w, gv[u].w));
+            }
         }
+    } else {
+        for (int i0 = 0; i0 < MT * K; i0 += 256 * 16) {
+            float v[16], gv[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int i = i0 + 256 * u + tid;
-            const int t = i / K, k = i - t * K;
-            if (i < MT * K)
-                xs[t * tstride + (k >> 8) * kGemvSbStride + (k & 255)] =
-                    gate ? v[u] * (1.0f / (1.0f + expf(-gv[u]))) : v[u];
+            for (int u = 0; u < 16; ++u) {
+                const int i = i0 + 256 * u + tid;
+                const int t = i / K, k = i - t * K;
+                const bool ok = i < MT * K && t < M;
+                v[u] = ok ? reinterpret_cast<const float *>(x + t * x_nb1)[k] : 0.0f;
+                gv[u] = ok && gate ? reinterpret_cast<const float *>(gate + t * g_nb1)[k] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int i = i0 + 256 * u + tid;
+                const int t = i / K, k = i - t * K;
+                if (i < MT * K) xs[t * tstride + (k >> 8) * kGemvSbStride + (k & 255)] = gated(v[u], gv[u]);
+            }
         }
     }
     __syncthreads();
     for (int i = tid; i < MT * (K / 32); i += 256) {
         const int t = i / (K / 32), sub = i - t * (K / 32);
-        const float *src = xs + t * tstride + (sub >> 3) * kGemvSbStride + 32 * (sub & 7);
+        const float4 *src = reinterpret_cast<const float4 *>(xs + t * tstride + (sub >> 3) * kGemvSbStride + 32 * (sub & 7));
         float a = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 32; ++j) a += src[j];
+        for (int j = 0; j < 8; ++j) {
+            const float4 f = src[j];
+            a += (f.x + f.y) + (f.z + f.w);
+        }
         ssum[i] = a;
     }
     __syncthreads();
     float acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
+    // x * (code 2^-24) + acc, the code in the low (SEL 0) or high (SEL 1) fp16 half of c
+#define SQA_MIX(ACC, X, C, SEL)                                                                           \
+    asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[0," #SEL ",0] op_sel_hi:[0,1,0]" : "+v"(ACC) : "v"(X), "v"(C))
     for (int sb = l32 >> 1; sb < nsb; sb += 16) {
         if (sb != (l32 >> 1)) load_w(sb);
         const float d = h2f(hdr.x & 0xffffu), dmin = h2f(hdr.x >> 16);
-        const uint32_t *qw = &qb[0].x;  // 16 dwords: code bytes of groups 2h, 2h+1
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
             const int j = 2 * hj + jj;  // sub-blocks 2j (low nibbles) and 2j+1 (high)
@@ -713,23 +747,29 @@ __global__ __launch_bounds__(256) void op_gemv_kernel(const uint8_t *__restrict_
             const float *xl = xs + sb * kGemvSbStride + 64 * j;
 #pragma unroll
             for (int m = 0; m < 8; ++m) {
-                const uint32_t q = qw[8 * jj + m];  // code bytes 32j + 4m .. +3
+                // code bytes 32j + 4m .. +3: dword m of the group's 32 bytes
+                const uint4 qv = qb[2 * jj + (m >> 2)];
+                const uint32_t q = (m & 3) == 0 ? qv.x : (m & 3) == 1 ? qv.y : (m & 3) == 2 ? qv.z : qv.w;
+                const uint32_t c02 = q & 0x000F000Fu;           // low nibbles of bytes 0, 2
+                const uint32_t c13 = (q >> 8) & 0x000F000Fu;    // of bytes 1, 3
+                const uint32_t h02 = (q >> 4) & 0x000F000Fu;    // high nibbles of bytes 0, 2
+                const uint32_t h13 = (q >> 12) & 0x000F000Fu;   // of bytes 1, 3
 #pragma unroll
                 for (int t = 0; t < MT; ++t) {
                     const float4 xa = *reinterpret_cast<const float4 *>(xl + t * tstride + 4 * m);
                     const float4 xb = *reinterpret_cast<const float4 *>(xl + t * tstride + 32 + 4 * m);
-                    dl[t] = fmaf((float)(q & 15), xa.x, dl[t]);
-                    dl[t] = fmaf((float)((q >> 8) & 15), xa.y, dl[t]);
-                    dl[t] = fmaf((float)((q >> 16) & 15), xa.z, dl[t]);
-                    dl[t] = fmaf((float)((q >> 24) & 15), xa.w, dl[t]);
-                    dh[t] = fmaf((float)((q >> 4) & 15), xb.x, dh[t]);
-                    dh[t] = fmaf((float)((q >> 12) & 15), xb.y, dh[t]);
-                    dh[t] = fmaf((float)((q >> 20) & 15), xb.z, dh[t]);
-                    dh[t] = fmaf((float)(q >> 28), xb.w, dh[t]);
+                    SQA_MIX(dl[t], xa.x, c02, 0);
+                    SQA_MIX(dl[t], xa.y, c13, 0);
+                    SQA_MIX(dl[t], xa.z, c02, 1);
+                    SQA_MIX(dl[t], xa.w, c13, 1);
+                    SQA_MIX(dh[t], xb.x, h02, 0);
+                    SQA_MIX(dh[t], xb.y, h13, 0);
+                    SQA_MIX(dh[t], xb.z, h02, 1);
+                    SQA_MIX(dh[t], xb.w, h13, 1);
                 }
             }
-            const float s0 = d * (float)sc0, m0 = dmin * (float)mn0;
-            const float s1 = d * (float)sc1, m1 = dmin * (float)mn1;
+            const float s0 = d * (float)sc0 * 16777216.0f, m0 = dmin * (float)mn0;
+            const float s1 = d * (float)sc1 * 16777216.0f, m1 = dmin * (float)mn1;
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
                 const float *st = ssum + t * (K / 32) + sb * kSubs + 2 * j;
@@ -740,11 +780,18 @@ __global__ __launch_bounds__(256) void op_gemv_kernel(const uint8_t *__restrict_
             }
         }
     }
-    // the 32 threads of a row are 32 consecutive lanes
+#undef SQA_MIX
+    // the 32 threads of a row are 32 consecutive lanes: DPP rotations inside each
+    // 16-lane row, then the partner row (lane ^ 16)
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-#pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) acc[t] += __shfl_xor(acc[t], o);
+        float a = acc[t];
+        a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x128, 0xf, 0xf, false));  // row_ror:8
+        a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x124, 0xf, 0xf, false));  // row_ror:4
+        a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x122, 0xf, 0xf, false));  // row_ror:2
+        a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x121, 0xf, 0xf, false));  // row_ror:1
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+        acc[t] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
     if (l32 == 0 && row < N) {
 #pragma unroll
@@ -787,8 +834,9 @@ int launch_out_proj(const sqa_tensor &w, const sqa_tensor &x, const sqa_tensor *
         static std::once_flag lds_once;  // up to 4 x 16K floats of activations
         static hipError_t lds_err = hipSuccess;
         std::call_once(lds_once, [] {
-            for (const void *f : {(const void *)op_gemv_kernel<1>, (const void *)op_gemv_kernel<2>,
-                                  (const void *)op_gemv_kernel<4>})
+            for (const void *f : {(const void *)op_gemv_kernel<1, true>, (const void *)op_gemv_kernel<2, true>,
+                                  (const void *)op_gemv_kernel<4, true>, (const void *)op_gemv_kernel<1, false>,
+                                  (const void *)op_gemv_kernel<2, false>, (const void *)op_gemv_kernel<4, false>})
                 if (lds_err == hipSuccess)
                     lds_err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kGemvMaxLds);
         });
@@ -804,12 +852,17 @@ int launch_out_proj(const sqa_tensor &w, const sqa_tensor &x, const sqa_tensor *
         float *dd = (float *)dst.data;
         const int64_t dn = (int64_t)dst.nb[1];
         const dim3 grid((unsigned)(N / 8));
+        const bool vec = (uintptr_t)xd % 16 == 0 && xn % 16 == 0 && (!gd || ((uintptr_t)gd % 16 == 0 && gn % 16 == 0));
+#define SQA_GEMV(MTV)                                                                                          \
+    (vec ? op_gemv_kernel<MTV, true> : op_gemv_kernel<MTV, false>)<<<grid, dim3(256), lds, s>>>(               \
+        wd, wn, xd, xn, gd, gn, (int)K, (int)N, (int)M, dd, dn)
         if (mt == 1)
-            op_gemv_kernel<1><<<grid, dim3(256), lds, s>>>(wd, wn, xd, xn, gd, gn, (int)K, (int)N, (int)M, dd, dn);
+            SQA_GEMV(1);
         else if (mt == 2)
-            op_gemv_kernel<2><<<grid, dim3(256), lds, s>>>(wd, wn, xd, xn, gd, gn, (int)K, (int)N, (int)M, dd, dn);
+            SQA_GEMV(2);
         else
-            op_gemv_kernel<4><<<grid, dim3(256), lds, s>>>(wd, wn, xd, xn, gd, gn, (int)K, (int)N, (int)M, dd, dn);
+            SQA_GEMV(4);
+#undef SQA_GEMV
         profile_stop(prof, s);
         return hip_status(hipGetLastError(), "out_proj launch");
     }
