@@ -184,7 +184,8 @@ int sqa_supports_flash_attn_ext(const sqa_tensor *q, const sqa_tensor *k, const 
 
 /*
  * Allocation-free form of sqa_flash_attn_ext for decode/verify shapes (up to 4
- * positions and 16 query rows per KV head, 2 KV heads, 16-byte aligned q rows).
+ * positions and 16 query rows per KV head, any number of KV heads, 16-byte
+ * aligned q rows).
  * It has no counterpart in the reference: it is for callers that cannot
  * allocate or pass a workspace (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). Its scratch is a device array of

@@ -95,8 +95,8 @@ int check_fa(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
     const int64_t G = q->ne[2] / k->ne[2];
     const bool q_aligned = (uintptr_t)q->data % 16 == 0 && q->nb[1] % 16 == 0 && q->nb[2] % 16 == 0;
     // the split-KV decode kernel: up to 4 positions and 16 query rows per KV head,
-    // two KV heads, 16-byte aligned q rows; everything else runs as a prefill chunk
-    *decode = q->ne[1] <= 4 && q->ne[1] * G <= 16 && k->ne[2] == 2 && q_aligned;
+    // 16-byte aligned q rows; everything else runs as a prefill chunk
+    *decode = q->ne[1] <= 4 && q->ne[1] * G <= 16 && q_aligned;
     if (!*decode && 16 % G != 0)
         return set_error(SQA_ERR_UNSUPPORTED, "flash_attn_ext: prefill needs n_head/n_head_kv to divide 16");
     return SQA_OK;
@@ -122,7 +122,7 @@ int check_mask(const sqa_tensor *mask, const sqa_tensor *q, const sqa_tensor *k)
 
 size_t fa_workspace(const sqa_tensor *q, const sqa_tensor *k, bool decode) {
     const int64_t n_q = q->ne[1], H = q->ne[2], n_kv = k->ne[1], Hkv = k->ne[2];
-    return decode ? fa_decode_workspace(n_q, H, n_kv) : fa_prefill_workspace(n_q, H, Hkv, n_kv);
+    return decode ? fa_decode_workspace(n_q, H, Hkv, n_kv) : fa_prefill_workspace(n_q, H, Hkv, n_kv);
 }
 
 int run_fa(const FaArgs &a, bool decode, hipStream_t s) {
@@ -316,8 +316,8 @@ int sqa_flash_attn_ext_static(const sqa_tensor *q, const sqa_tensor *k, const sq
     if (!decode)
         return set_error(SQA_ERR_UNSUPPORTED,
                          "flash_attn_ext_static: only decode/verify shapes (up to 4 positions and 16 query "
-                         "rows per KV head, 2 KV heads, 16-byte aligned q rows); use sqa_flash_attn_ext");
-    const size_t need = fa_decode_workspace(q->ne[1], q->ne[2], k->ne[1]);
+                         "rows per KV head, 16-byte aligned q rows); use sqa_flash_attn_ext");
+    const size_t need = fa_decode_workspace(q->ne[1], q->ne[2], k->ne[2], k->ne[1]);
     if (need > kStaticScratchBytes)
         return set_error(SQA_ERR_WORKSPACE,
                          "flash_attn_ext_static: these shapes need %zu bytes of scratch, above its %zu-byte "

@@ -46,7 +46,7 @@ struct FaArgs {
     void *ws;
     size_t ws_bytes;
 };
-size_t fa_decode_workspace(int64_t n_q, int64_t H, int64_t n_kv);
+size_t fa_decode_workspace(int64_t n_q, int64_t H, int64_t n_kvh, int64_t n_kv);
 // Device scratch of the allocation-free decode entry point: its size, and its
 // address on the current device (looked up once per device).
 constexpr size_t kStaticScratchBytes = SQA_STATIC_SCRATCH_BYTES;

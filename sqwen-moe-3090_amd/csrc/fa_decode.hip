@@ -1,17 +1,17 @@
 // fa_decode.hip - split-KV FlashAttention over a q4_0 K/V cache for decode and
 // speculative verify (n_q <= 4 positions, n_q * H/Hkv <= 16 query rows per KV
-// head, 2 KV heads).
+// head, any number of KV heads).
 //
 // Replaces the ggml FLASH_ATTN_EXT node built at src/model/attn.rs:228-251 of
 // the reference for n_q = 1..2 (decode step, MTP verify of runner.rs:1263-1270).
 //
 // Work split
-//   The key range is cut into one split per CU. Each split is served by two
-//   workgroups, one per KV head, that the dispatcher places on the same XCD
-//   (so the cache lines the two heads share in a 288-byte row are fetched from
-//   HBM once and served to the second workgroup by that XCD's L2); two such
-//   workgroups fit on a CU, so one head's wavefronts can issue while the
-//   other's wait at their barrier. Of the two workgroups on a CU the one
+//   The key range is cut into splits, about two workgroups per CU in all. Each
+//   split is served by one workgroup per KV head, all placed by the dispatcher
+//   on the same XCD (so the cache lines the heads share in a cache row of
+//   Hkv x 144 bytes are fetched from HBM once and served to the other heads'
+//   workgroups by that XCD's L2); two workgroups fit on a CU, so one's
+//   wavefronts can issue while the other's wait at their barrier. Of the two workgroups on a CU the one
 //   dispatched first wins the issue arbitration (older wavefronts go first)
 //   and runs about twice as fast while both are resident, so the splits of
 //   the first dispatch round take twice the tiles of the second: both rounds
@@ -92,7 +92,6 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kTileKeys = 64;
 constexpr int kKStages = 3;
 constexpr int kVStages = 3;
-constexpr int kCacheRow = 2 * kHeadRowBytes;          // 288: one cache row, both KV heads
 constexpr int kSlotsPerRow = 10;                      // 9 data chunks + a pad chunk
 constexpr int kLdsRow = 16 * kSlotsPerRow;            // 160
 constexpr int kTensorBytes = kTileKeys * kLdsRow;     // 10240
@@ -233,7 +232,9 @@ __device__ __forceinline__ float exp2_or_zero(float a, float b) {  // 2^(a-b), 0
 }
 
 struct DecodeParams {
-    const uint8_t *k, *v;   // cache rows of 288 bytes (both KV heads), row stride 288
+    const uint8_t *k, *v;   // cache rows of row_bytes = n_kvh x 144 bytes (all KV heads)
+    int64_t row_bytes;
+    int n_kvh;              // KV heads
     const char *q;          // F32, row (t, h) at q + t*q_nb1 + h*q_nb2, 16-byte aligned
     int64_t q_nb1, q_nb2;
     const char *mask;       // F16 [n_kv] per query row, 16-byte aligned rows, or null
@@ -262,13 +263,13 @@ __device__ __forceinline__ int v_rot(int row) { return 2 * ((row >> 3) & 3); }
 // lane lands at LDS byte 16*s, i.e. slot s % 10 of row s / 10, and holds chunk
 // (slot - rot) mod 10 of that row's head half (chunk 9, the pad, repeats chunk 8).
 template <bool V>
-__device__ __forceinline__ uint32_t slot_offset(int j, int lane, int kvh) {
+__device__ __forceinline__ uint32_t slot_offset(int j, int lane, int kvh, uint32_t row_bytes) {
     const int s = 64 * j + lane;
     const int row = s / kSlotsPerRow;
     const int slot = s - row * kSlotsPerRow;
     int c = slot - (V ? v_rot(row) : k_rot(row));
     c = c < 0 ? c + kSlotsPerRow : c;
-    return (uint32_t)(row * kCacheRow + kvh * kHeadRowBytes + (c < 8 ? c : 8) * 16);
+    return (uint32_t)row * row_bytes + (uint32_t)(kvh * kHeadRowBytes + (c < 8 ? c : 8) * 16);
 }
 // LDS byte of head-row byte c (0..143) of row `row` inside a tile stage
 template <bool V>
@@ -300,11 +301,13 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
     constexpr int kRowMask = TWO ? 15 : 7;  // rows 8-15 mirror rows 0-7 when only 8 exist
 
     // ---------------- split and KV head of this workgroup ---------------------
-    // Workgroups go round-robin to the 8 XCDs: ids 16a + 8h + x (x < 8) are split
-    // 8a + x, head h, so both heads of a split share an XCD (and its L2).
+    // Workgroups go round-robin to the 8 XCDs: ids 8 Hkv a + 8h + x (x < 8) are
+    // split 8a + x, head h, so all heads of a split share an XCD (and its L2).
     const int id = blockIdx.x;
-    const int kvh = (id >> 3) & 1;
-    const int split = ((id >> 4) << 3) | (id & 7);
+    const int hb = id >> 3;
+    const int sa = hb / p.n_kvh;
+    const int kvh = hb - sa * p.n_kvh;
+    const int split = (sa << 3) | (id & 7);
     auto cw = [&](int s) -> int64_t {
         return s < p.n_first ? (int64_t)p.w_first * s
                              : (int64_t)p.w_first * p.n_first + (int64_t)p.w_second * (s - p.n_first);
@@ -629,8 +632,8 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         for (int r = 0; r < 3; ++r) {
             const int jk = vw + 4 * r;
             const int jv = ((vw + 2) & 3) + 4 * r;
-            koff[r] = slot_offset<false>(jk < kTensorInsts ? jk : 0, lane, kvh);
-            voff[r] = slot_offset<true>(jv < kTensorInsts ? jv : 0, lane, kvh);
+            koff[r] = slot_offset<false>(jk < kTensorInsts ? jk : 0, lane, kvh, (uint32_t)p.row_bytes);
+            voff[r] = slot_offset<true>(jv < kTensorInsts ? jv : 0, lane, kvh, (uint32_t)p.row_bytes);
             nk += jk < kTensorInsts;
             nv += jv < kTensorInsts;
         }
@@ -643,7 +646,7 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         // keys past the cache end re-read its last row (they are masked off); mask
         // segments past the readable length re-read its last 16 bytes
         auto lim_of = [&](int64_t kt) -> uint32_t {
-            return p.n_kv - kt >= kTileKeys ? 0xFFFFFFFFu : (uint32_t)((p.n_kv - kt) * kCacheRow - 16);
+            return p.n_kv - kt >= kTileKeys ? 0xFFFFFFFFu : (uint32_t)((p.n_kv - kt) * p.row_bytes - 16);
         };
         auto mlim_of = [&](int64_t kt) -> uint32_t {
             return p.mask_len - kt >= kTileKeys + 8 ? 0xFFFFFFFFu : (uint32_t)((p.mask_len - 8 - kt) * 2);
@@ -656,12 +659,13 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             const int64_t y = p.mask_len - k0 - (kTileKeys + 8);
             t_fast = y < 0 ? 0 : (int)min((int64_t)t_fast, y / kTileKeys + 1);
         }
-        const uint8_t *kb0 = p.k + k0 * kCacheRow;
-        const uint8_t *vb0 = p.v + k0 * kCacheRow;
+        const uint8_t *kb0 = p.k + k0 * p.row_bytes;
+        const uint8_t *vb0 = p.v + k0 * p.row_bytes;
+        const int64_t tile_bytes = kTileKeys * p.row_bytes;
         const char *mb0 = p.mask ? p.mask + k0 * 2 : nullptr;
         const bool mask_lane = mask_dma && mrow_l < p.n_q;
         auto issue_k = [&](int t, int st) {  // st = t mod kKStages
-            const uint8_t *kb = kb0 + (int64_t)t * (kTileKeys * kCacheRow);
+            const uint8_t *kb = kb0 + (int64_t)t * tile_bytes;
             const uint32_t kbase = lds0 + st * kTensorBytes;
             const uint32_t mdst = lds0 + kOffMask + st * kMaskStageBytes;
             if (t < t_fast) {
@@ -683,7 +687,7 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             }
         };
         auto issue_v = [&](int t, int st) {  // st = t mod kVStages
-            const uint8_t *vb = vb0 + (int64_t)t * (kTileKeys * kCacheRow);
+            const uint8_t *vb = vb0 + (int64_t)t * tile_bytes;
             const uint32_t vbase = lds0 + kOffV + st * kTensorBytes;
             const uint32_t lim = t < t_fast ? 0xFFFFFFFFu : lim_of(k0 + (int64_t)t * kTileKeys);
 #pragma unroll
@@ -986,11 +990,12 @@ __global__ __launch_bounds__(256) void mask_pack_kernel(const char *__restrict__
     }
 }
 
-// One split per CU, a multiple of 8 so that the workgroup numbering above holds
-// (at most kMaxSplits); at least ~4 tiles per split.
-int decode_splits(int64_t n_kv) {
+// About two workgroups per CU over all KV heads (one split per CU at 2 KV
+// heads), a multiple of 8 so that the workgroup numbering above holds (at most
+// kMaxSplits); at least ~4 tiles per split.
+int decode_splits(int64_t n_kv, int64_t n_kvh) {
     const int64_t tiles = (n_kv + kTileKeys - 1) / kTileKeys;
-    int64_t cap = device_cu_count() / 8 * 8;
+    int64_t cap = 2 * device_cu_count() / n_kvh / 8 * 8;
     if (cap > kMaxSplits) cap = kMaxSplits;
     if (cap < 8) cap = 8;
     int64_t s = (tiles + 3) / 4;
@@ -1029,8 +1034,8 @@ int static_scratch(void **out) {
     return SQA_OK;
 }
 
-size_t fa_decode_workspace(int64_t n_q, int64_t H, int64_t n_kv) {
-    const int64_t splits = decode_splits(n_kv);
+size_t fa_decode_workspace(int64_t n_q, int64_t H, int64_t n_kvh, int64_t n_kv) {
+    const int64_t splits = decode_splits(n_kv, n_kvh);
     const size_t acc = al256((size_t)(splits * n_q * H * 256) * sizeof(float));
     const size_t ml = al256((size_t)(splits * n_q * H * 2) * sizeof(float));
     const size_t mask = al256((size_t)(n_q * ((n_kv + 7) / 8 * 8)) * 2);
@@ -1040,11 +1045,12 @@ size_t fa_decode_workspace(int64_t n_q, int64_t H, int64_t n_kv) {
 int launch_fa_decode(const FaArgs &a, hipStream_t s) {
     const sqa_tensor &q = *a.q, &k = *a.k;
     const int64_t n_q = q.ne[1], H = q.ne[2], n_kv = k.ne[1], Hkv = k.ne[2];
-    if (Hkv != 2) return set_error(SQA_ERR_UNSUPPORTED, "decode kernel built for 2 KV heads");
     if (n_q > kMaxMaskRows) return set_error(SQA_ERR_UNSUPPORTED, "decode kernel takes at most 4 query positions");
     DecodeParams p;
     p.k = (const uint8_t *)k.data;
     p.v = (const uint8_t *)a.v->data;
+    p.row_bytes = (int64_t)k.nb[1];  // n_kvh x 144, checked by the caller
+    p.n_kvh = (int)Hkv;
     p.q = (const char *)q.data;
     p.q_nb1 = (int64_t)q.nb[1];
     p.q_nb2 = (int64_t)q.nb[2];
@@ -1055,21 +1061,21 @@ int launch_fa_decode(const FaArgs &a, hipStream_t s) {
     p.rows = (int)(n_q * p.G);
     p.n_kv = n_kv;
     p.qscale = a.scale * kLog2e;
-    p.n_splits = decode_splits(n_kv);
+    p.n_splits = decode_splits(n_kv, Hkv);
     // whole 64-key tiles per split: no tile is read by two splits. With two
     // workgroups per CU, the ones dispatched first (ids below the CU count, i.e.
-    // splits below half of it) issue ahead of the second round on the same CU
+    // splits below CUs / Hkv) issue ahead of the second round on the same CU
     // (the older wavefront wins the arbitration) and run faster: they take the
     // larger share, kFirstRoundWeight : kSecondRoundWeight, so that both rounds
     // end together instead of the second running on alone.
     p.tiles = (n_kv + kTileKeys - 1) / kTileKeys;
     const int cus = device_cu_count();
-    p.n_first = 2 * p.n_splits > cus ? cus / 2 : p.n_splits;
+    p.n_first = Hkv * p.n_splits > cus ? (int)(cus / Hkv) : p.n_splits;
     if (p.n_first > p.n_splits) p.n_first = p.n_splits;
     p.w_first = p.n_first < p.n_splits ? kFirstRoundWeight : 1;
     p.w_second = p.n_first < p.n_splits ? kSecondRoundWeight : 1;
     p.cw_total = (int64_t)p.w_first * p.n_first + (int64_t)p.w_second * (p.n_splits - p.n_first);
-    const size_t need = fa_decode_workspace(n_q, H, n_kv);
+    const size_t need = fa_decode_workspace(n_q, H, Hkv, n_kv);
     if (!a.ws || a.ws_bytes < need)
         return set_error(SQA_ERR_WORKSPACE, "flash_attn_ext: workspace %zu bytes < %zu needed", a.ws_bytes, need);
     uint8_t *wsb = reinterpret_cast<uint8_t *>(((uintptr_t)a.ws + 255) & ~(uintptr_t)255);
@@ -1108,7 +1114,7 @@ int launch_fa_decode(const FaArgs &a, hipStream_t s) {
                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     });
     if (lds_err != hipSuccess) return hip_status(lds_err, "fa_decode LDS attribute");
-    const unsigned grid = (unsigned)(2 * p.n_splits);  // (split, KV head) pairs
+    const unsigned grid = (unsigned)(Hkv * p.n_splits);  // (split, KV head) pairs
     const int prof = profile_start("fa_decode", s);
     if (p.rows <= 8)
         fa_decode_kernel<false><<<dim3(grid), dim3(kThreads), kLdsBytes, s>>>(p);

@@ -77,6 +77,26 @@ def test_decode_kernel_other_group_sizes(sqa, orc, dev, H, n_q, n_kv):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("Hkv,H,n_q,n_kv", [(1, 16, 1, 3000), (1, 8, 2, 70000), (4, 16, 2, 20000),
+                                            (8, 16, 1, 5000), (8, 32, 4, 1500), (16, 16, 1, 999)])
+def test_decode_kernel_other_kv_head_counts(sqa, orc, dev, Hkv, H, n_q, n_kv):
+    """Any number of KV heads: cache rows of Hkv x 144 bytes, G = H/Hkv query
+    heads per KV head, splits scaled to about two workgroups per CU (capped at
+    256 splits for one KV head, 32 splits at 16 KV heads)."""
+    q, kq, vq = qkv(orc, 57 + Hkv + H + n_q, n_q, n_kv, H=H, Hkv=Hkv, outliers=3)
+    mask = orc.causal_mask(n_q, n_kv, n_kv - n_q)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    sqa.profile_begin(16)
+    try:
+        got = run_gpu(sqa, dev, q, kq, vq, mask)
+    finally:
+        sqa.profile_end()
+    assert sqa.profile_get("fa_decode")[1] == 1, "expected the decode kernel for this shape"
+    err = rel_err(got, ref)
+    print(f"decode Hkv={Hkv} H={H} n_q={n_q} n_kv={n_kv}: max err / rms = {err:.3e}")
+    assert err <= TOL
+
+
 def test_finite_mask_values_and_fully_masked_row(sqa, orc, dev):
     q, kq, vq = qkv(orc, 11, 2, 700)
     rng = np.random.default_rng(12)
