@@ -528,23 +528,44 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             // d_k of the lane's four C rows 16kg + 4g + i, block b: 8 bytes at
             // Dk[b][16kg + 4g]
             const uint8_t *dkb = smem + (t & 1) * kKStage + kOffDk + 8 * g;
+            // Software-pipelined by one step: step j = (block j >> 1, key group j & 1)
+            // issues its MFMAs, then the d_k scaling of step j - 1 runs while they
+            // execute. The scheduling barrier keeps the compiler from pulling the
+            // scaling back next to the MFMAs it reads (it did, leaving 4-12
+            // instructions between an MFMA and its consumer). The sum into sa keeps
+            // the block order of the plain loop.
+            floatx4 cp[kRG];
+            uint2 dkp;
 #pragma unroll
-            for (int b = 0; b < 8; ++b) {
-#pragma unroll
-                for (int kg = 0; kg < 2; ++kg) {
+            for (int j = 0; j <= 16; ++j) {
+                floatx4 cn[kRG];
+                uint2 dkn;
+                if (j < 16) {
+                    const int b = j >> 1, kg = j & 1;
                     const int o = kg * 8192 + 128 * (b >> 1);
                     const half8 ak = lds_half8(smem, kb[b & 1][0] + o, kb[b & 1][1] + o);
-                    const uint2 dk2 = *reinterpret_cast<const uint2 *>(dkb + 64 * b + 32 * kg);
-                    _Float16 dk[4];
-                    __builtin_memcpy(dk, &dk2, 8);
+                    dkn = *reinterpret_cast<const uint2 *>(dkb + 64 * b + 32 * kg);
 #pragma unroll
                     for (int rg = 0; rg < kRG; ++rg) {
-                        floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bqh[rg][b],
-                                                                           floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bql[rg][b], c, 0, 0, 0);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) sa[rg][kg][i] = fmaf(c[i], (float)dk[i], sa[rg][kg][i]);
+                        const floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bqh[rg][b],
+                                                                                 floatx4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        cn[rg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ak, bql[rg][b], c, 0, 0, 0);
                     }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (j > 0) {
+                    const int kg = (j - 1) & 1;
+                    _Float16 dk[4];
+                    __builtin_memcpy(dk, &dkp, 8);
+#pragma unroll
+                    for (int rg = 0; rg < kRG; ++rg)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) sa[rg][kg][i] = fmaf(cp[rg][i], (float)dk[i], sa[rg][kg][i]);
+                }
+                if (j < 16) {
+                    dkp = dkn;
+#pragma unroll
+                    for (int rg = 0; rg < kRG; ++rg) cp[rg] = cn[rg];
                 }
             }
             float s[kRG][8];  // keys 8g + jj, base-2 logits
