@@ -397,10 +397,12 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
     const uint32_t m_row =
         has_m ? (uint32_t)((int64_t)(q_base + m_r < p.n_q ? q_base + m_r : p.n_q - 1) * p.mask_nb1) : 0u;
     const bool m_lane = m_r < p.qb;
+    // record of the split's first tile (k_begin is a multiple of kPK); tile t's
+    // record is t records further on
+    const uint8_t *rec0 = kv_h + (k_begin / kPK) * kTileBytes;
     auto issue = [&](int t_k, int t_v) {  // tile indices or -1
         if (t_k >= 0) {
-            const int64_t kt = k_begin + (int64_t)t_k * kPK;
-            const uint8_t *rec = kv_h + (kt / kPK) * kTileBytes;
+            const uint8_t *rec = rec0 + (int64_t)t_k * kTileBytes;
             const uint32_t st = lds0 + (uint32_t)((t_k & 1) * kKStage);
 #pragma unroll
             for (int i = 0; i < 3; ++i) {
@@ -409,14 +411,14 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                     dma16(1024u * jj + 16u * lane, rec, st + 1024u * jj);
             }
             if (has_m) {
+                const int64_t kt = k_begin + (int64_t)t_k * kPK;
                 const int64_t col = kt + 8 * m_c < p.mask_len ? kt + 8 * m_c : p.mask_len - 8;
                 const uint32_t sm = lds0 + (uint32_t)(kLdsMask + (t_k & 1) * p.mask_stage + 1024 * jm);
                 if (m_lane) dma16(m_row + (uint32_t)(2 * col), p.mask, sm);
             }
         }
         if (t_v >= 0) {
-            const int64_t kt = k_begin + (int64_t)t_v * kPK;
-            const uint8_t *rec = kv_h + (kt / kPK) * kTileBytes + kKHalf;
+            const uint8_t *rec = rec0 + (int64_t)t_v * kTileBytes + kKHalf;
             const uint32_t st = lds0 + (uint32_t)(kLdsV + (t_v & 1) * kVStage);
 #pragma unroll
             for (int i = 0; i < 3; ++i) {
