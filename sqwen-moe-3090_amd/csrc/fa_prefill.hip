@@ -390,6 +390,8 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
     const uint8_t *kv_h = p.kv + (int64_t)kvh * p.kv_tiles * kTileBytes;
     const int jk0 = wave, jv0 = (wave + 4) % kWaves, jm = (wave + kWaves - 2) % kWaves;
     const bool has_m = jm < n_mask_inst;
+    static_assert(kKInst == 2 * kWaves + 1 && kVInst == 2 * kWaves + 1, "two full DMA instructions per wave and half");
+    const bool k_half = jk0 == 0, v_half = jv0 == 0;  // the wave that issues the 512-byte instruction
     // mask row of this lane's slot in instruction jm: position q_base + r (clamped
     // to n_q - 1), chunk c = (s & 3) ^ ((r >> 1) & 3) of the row's 32 keys
     const int m_r = (64 * jm + lane) >> 2;
@@ -404,12 +406,10 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
         if (t_k >= 0) {
             const uint8_t *rec = rec0 + (int64_t)t_k * kTileBytes;
             const uint32_t st = lds0 + (uint32_t)((t_k & 1) * kKStage);
-#pragma unroll
-            for (int i = 0; i < 3; ++i) {
-                const int jj = jk0 + kWaves * i;
-                if (jj < kKInst - 1 || (jj == kKInst - 1 && lane < 32))
-                    dma16(1024u * jj + 16u * lane, rec, st + 1024u * jj);
-            }
+            // instructions jk0 and jk0 + 8 (full), and 16 (512 bytes) on wave 0
+            dma16(1024u * jk0 + 16u * lane, rec, st + 1024u * jk0);
+            dma16(1024u * (jk0 + kWaves) + 16u * lane, rec, st + 1024u * (jk0 + kWaves));
+            if (k_half && lane < 32) dma16(1024u * (kKInst - 1) + 16u * lane, rec, st + 1024u * (kKInst - 1));
             if (has_m) {
                 const int64_t kt = k_begin + (int64_t)t_k * kPK;
                 const int64_t col = kt + 8 * m_c < p.mask_len ? kt + 8 * m_c : p.mask_len - 8;
@@ -420,12 +420,9 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
         if (t_v >= 0) {
             const uint8_t *rec = rec0 + (int64_t)t_v * kTileBytes + kKHalf;
             const uint32_t st = lds0 + (uint32_t)(kLdsV + (t_v & 1) * kVStage);
-#pragma unroll
-            for (int i = 0; i < 3; ++i) {
-                const int jj = jv0 + kWaves * i;
-                if (jj < kVInst - 1 || (jj == kVInst - 1 && lane < 32))
-                    dma16(1024u * jj + 16u * lane, rec, st + 1024u * jj);
-            }
+            dma16(1024u * jv0 + 16u * lane, rec, st + 1024u * jv0);
+            dma16(1024u * (jv0 + kWaves) + 16u * lane, rec, st + 1024u * (jv0 + kWaves));
+            if (v_half && lane < 32) dma16(1024u * (kVInst - 1) + 16u * lane, rec, st + 1024u * (kVInst - 1));
         }
     };
     if (n_tiles > 0) issue(0, -1);
