@@ -138,23 +138,6 @@ __device__ __forceinline__ void dma16(uint32_t voff, const void *sbase, uint32_t
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(bs), "s"(ms) : "memory");
 }
 
-// Wait until at most n vector-memory loads of this wavefront are outstanding
-// and its LDS accesses are done, then synchronise the workgroup. n is
-// wave-uniform and small.
-__device__ __forceinline__ void wait_vm_barrier(int n) {
-    // a switch on a value the compiler deems divergent would run several cases,
-    // i.e. several barriers, under partial exec masks: force it scalar
-    switch (__builtin_amdgcn_readfirstlane(n)) {
-#define SQA_WAIT_CASE(N) \
-    case N: asm volatile("s_waitcnt vmcnt(" #N ") lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
-        SQA_WAIT_CASE(0) SQA_WAIT_CASE(1) SQA_WAIT_CASE(2) SQA_WAIT_CASE(3) SQA_WAIT_CASE(4)
-        SQA_WAIT_CASE(5) SQA_WAIT_CASE(6) SQA_WAIT_CASE(7) SQA_WAIT_CASE(8) SQA_WAIT_CASE(9)
-        SQA_WAIT_CASE(10) SQA_WAIT_CASE(11) SQA_WAIT_CASE(12) SQA_WAIT_CASE(13) SQA_WAIT_CASE(14)
-#undef SQA_WAIT_CASE
-        default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
-    }
-}
-
 typedef const __attribute__((address_space(3))) uint32_t lds_u32;  // LDS dword from a raw LDS address
 
 __device__ __forceinline__ uint32_t lds32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
@@ -640,8 +623,9 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         const bool mask_dma = p.mask && vw == kValueWaves - 1;
         const int mrow_l = lane >> 3;  // mask DMA lane -> query row, 16-byte segment
         const uint32_t moff = (uint32_t)((int64_t)(mrow_l < p.n_q ? mrow_l : 0) * p.mask_nb1 + 16 * (lane & 7));
-        const int per_k = nk + (mask_dma ? 1 : 0);  // DMA instructions per K tile (wave-uniform)
-        const int per_v = nv;
+        // every wavefront issues 2 or 3 of the 10 K and of the 10 V instructions
+        static_assert(kTensorInsts == 10 && kValueWaves == 4, "2 or 3 instructions per wavefront and tensor");
+        const bool k3 = nk == 3, v3 = nv == 3;
 
         // keys past the cache end re-read its last row (they are masked off); mask
         // segments past the readable length re-read its last 16 bytes
@@ -664,21 +648,21 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         const int64_t tile_bytes = kTileKeys * p.row_bytes;
         const char *mb0 = p.mask ? p.mask + k0 * 2 : nullptr;
         const bool mask_lane = mask_dma && mrow_l < p.n_q;
-        auto issue_k = [&](int t, int st) {  // st = t mod kKStages
-            const uint8_t *kb = kb0 + (int64_t)t * tile_bytes;
+        // kb, vb: the tile's first cache row (the loop carries them, one add per tile)
+        auto issue_k = [&](int t, int st, const uint8_t *kb) {  // st = t mod kKStages
             const uint32_t kbase = lds0 + st * kTensorBytes;
             const uint32_t mdst = lds0 + kOffMask + st * kMaskStageBytes;
             if (t < t_fast) {
-#pragma unroll
-                for (int r = 0; r < 3; ++r)
-                    if (r < nk) dma16(koff[r], kb, kbase + 1024u * (vw + 4 * r));
+                dma16(koff[0], kb, kbase + 1024u * vw);
+                dma16(koff[1], kb, kbase + 1024u * (vw + 4));
+                if (k3) dma16(koff[2], kb, kbase + 1024u * (vw + 8));
                 if (mask_lane) dma16(moff, mb0 + (int64_t)t * (kTileKeys * 2), mdst);
             } else {
                 const int64_t kt = k0 + (int64_t)t * kTileKeys;
                 const uint32_t lim = lim_of(kt);
-#pragma unroll
-                for (int r = 0; r < 3; ++r)
-                    if (r < nk) dma16(koff[r] < lim ? koff[r] : lim, kb, kbase + 1024u * (vw + 4 * r));
+                dma16(koff[0] < lim ? koff[0] : lim, kb, kbase + 1024u * vw);
+                dma16(koff[1] < lim ? koff[1] : lim, kb, kbase + 1024u * (vw + 4));
+                if (k3) dma16(koff[2] < lim ? koff[2] : lim, kb, kbase + 1024u * (vw + 8));
                 if (mask_dma) {
                     const uint32_t mlim = mlim_of(kt);
                     const uint32_t mo = moff - 16 * (lane & 7) + ((16u * (lane & 7)) < mlim ? 16u * (lane & 7) : mlim);
@@ -686,29 +670,43 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                 }
             }
         };
-        auto issue_v = [&](int t, int st) {  // st = t mod kVStages
-            const uint8_t *vb = vb0 + (int64_t)t * tile_bytes;
+        auto issue_v = [&](int t, int st, const uint8_t *vb) {  // st = t mod kVStages
             const uint32_t vbase = lds0 + kOffV + st * kTensorBytes;
-            const uint32_t lim = t < t_fast ? 0xFFFFFFFFu : lim_of(k0 + (int64_t)t * kTileKeys);
-#pragma unroll
-            for (int r = 0; r < 3; ++r)
-                if (r < nv) dma16(voff[r] < lim ? voff[r] : lim, vb, vbase + 1024u * (((vw + 2) & 3) + 4 * r));
+            const int j0 = (vw + 2) & 3;
+            if (t < t_fast) {
+                dma16(voff[0], vb, vbase + 1024u * j0);
+                dma16(voff[1], vb, vbase + 1024u * (j0 + 4));
+                if (v3) dma16(voff[2], vb, vbase + 1024u * (j0 + 8));
+            } else {
+                const uint32_t lim = lim_of(k0 + (int64_t)t * kTileKeys);
+                dma16(voff[0] < lim ? voff[0] : lim, vb, vbase + 1024u * j0);
+                dma16(voff[1] < lim ? voff[1] : lim, vb, vbase + 1024u * (j0 + 4));
+                if (v3) dma16(voff[2] < lim ? voff[2] : lim, vb, vbase + 1024u * (j0 + 8));
+            }
         };
-        // DMA instructions this wavefront issued after the last one that interval t
-        // needs (K of tile t, V of tile t-1): the loop issues K(t+2) and V(t+1) at
-        // interval t, after K 0, K 1 and V 0 before the loop, so at interval t's
-        // barrier the younger ones are K(t+1) and V(t) (interval t-1's pair, or K 1
-        // and V 0 for t = 0).
-        auto younger_than_needed = [&](int t) -> int {
-            return (t + 1 < n_tiles ? per_k : 0) + (t < n_tiles ? per_v : 0);
+        // The wait at interval t: K of tile t and V of tile t-1 must have landed.
+        // The loop issues K(t+2) and V(t+1) at interval t, after K 0, K 1 and V 0
+        // before the loop, so the younger DMAs at interval t are K(t+1) and V(t):
+        // at least 2 + 2 + 1 = 5 instructions while t + 1 < n_tiles (each wavefront
+        // has 5 tensor instructions per tile pair, the mask wavefront one more), at
+        // least 2 (V(t)) when t + 1 == n_tiles, none at the end. Waiting down to
+        // that lower bound is exact for most wavefronts and, for the one with a
+        // sixth, also waits for the oldest of K(t+1), issued an interval earlier.
+        auto wait_interval = [&](int t) {
+            if (t + 1 < n_tiles)
+                asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            else if (t < n_tiles)
+                asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            else
+                asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         };
 
         // ---------------- K 0-1 and V 0 ------------------------------------------
         // (V stages 1-2 hold the Q operands until the loop's first barrier)
         static_assert(kKStages == 3 && kVStages == 3, "the stage counter below");
-        if (n_tiles > 0) issue_k(0, 0);
-        if (n_tiles > 1) issue_k(1, 1);
-        if (n_tiles > 0) issue_v(0, 0);
+        if (n_tiles > 0) issue_k(0, 0, kb0);
+        if (n_tiles > 1) issue_k(1, 1, kb0 + tile_bytes);
+        if (n_tiles > 0) issue_v(0, 0, vb0);
         if (!TWO) {
             // rows 8-15 of both P buffers (never written with 8 rows) hold zeros: the
             // residual operand of the lanes that carry hi parts (see the PV below)
@@ -776,12 +774,15 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         const _Float16 *const lrow0 = TWO ? arow0 + 64 : pbuf + (n ^ 8) * kPRow + 8 * g;
 
         int c = 0;  // t mod 3, carried through the loop (3 K and 3 V stages)
+        const uint8_t *kn = kb0 + 2 * tile_bytes, *vn = vb0 + tile_bytes;  // K(t+2), V(t+1)
         for (int tt = 0; tt <= n_tiles; ++tt) {
             const int t = TWO ? __builtin_amdgcn_readfirstlane(tt) : tt;  // wave-uniform tile index
             const int c1 = c == 2 ? 0 : c + 1, c2 = c == 0 ? 2 : c - 1;  // (t + 1) mod 3, (t + 2) mod 3
-            wait_vm_barrier(younger_than_needed(t));
-            if (t + 2 < n_tiles) issue_k(t + 2, c2);
-            if (t + 1 < n_tiles) issue_v(t + 1, c1);
+            wait_interval(t);
+            if (t + 2 < n_tiles) issue_k(t + 2, c2, kn);
+            if (t + 1 < n_tiles) issue_v(t + 1, c1, vn);
+            kn += tile_bytes;
+            vn += tile_bytes;
             c = c1;
             if (t == 0) continue;
 
