@@ -39,6 +39,16 @@ def test_static_entry_matches_workspace_entry(sqa, orc, dev):
     assert rel_err(got, orc.flash_attn_ext(q, kq, vq, None)) <= 2e-3
 
 
+@pytest.mark.parametrize("Hkv,H,n_q,n_kv", [(1, 16, 1, 20000), (8, 16, 2, 5000)])
+def test_static_entry_other_kv_head_counts(sqa, orc, dev, Hkv, H, n_q, n_kv):
+    """Other KV-head counts: more splits per head at one KV head, fewer at eight."""
+    q, kq, vq = qkv(orc, 64 + Hkv, n_q, n_kv, H=H, Hkv=Hkv)
+    mask = orc.causal_mask(n_q, n_kv, n_kv - n_q)
+    got, ref = _run_both(sqa, dev, q, kq, vq, mask)
+    assert np.array_equal(got, ref)
+    assert rel_err(got, orc.flash_attn_ext(q, kq, vq, mask)) <= 2e-3
+
+
 def test_static_entry_rejects_what_it_cannot_run(sqa, orc, dev):
     q, kq, vq = qkv(orc, 63, 8, 1024)  # 8 positions: a prefill chunk
     qt, kt, vt = (torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in (q, kq, vq))
