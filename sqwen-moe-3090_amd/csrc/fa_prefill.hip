@@ -135,6 +135,35 @@ __device__ __forceinline__ int key_row(int k) { return 16 * ((k >> 2) & 1) + 4 *
 //      threads 0..15 write the Dv rows and fold the largest |d_v| into
 //      dvmax[head] (fp16 magnitude bits, cleared by qprep_kernel, which runs
 //      first).
+// N dwords of a q4_0 block's qs bytes starting at byte off (2 mod 4 for even
+// blocks, 0 mod 4 for odd ones) of an LDS row: aligned reads, shifted by
+// alignbit. Every read stays inside the row's 144 bytes.
+template <int N = 4>
+__device__ __forceinline__ void qs_dwords(const uint8_t *row, int off, uint32_t *q) {
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(row + (off & ~3));
+    const uint32_t sh = 8u * (uint32_t)(off & 3);
+    uint32_t a = p[0];
+#pragma unroll
+    for (int m = 0; m < N; ++m) {
+        const uint32_t b = p[sh ? m + 1 : (m + 1 < N ? m + 1 : m)];
+        q[m] = __builtin_amdgcn_alignbit(b, a, sh);
+        a = b;
+    }
+}
+
+// Two 4-bit codes n (bits 0-3 and 16-19 of x) as the packed fp16 pair n - 8:
+// 0x6400 | n is exactly 1024 + n, and 1024 + n - 1032 is exact.
+__device__ __forceinline__ uint32_t codes_f16(uint32_t x) {
+    const uint32_t y = (x & 0x000F000Fu) | 0x64006400u;
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    h2 v;
+    __builtin_memcpy(&v, &y, 4);
+    const h2 d = v + h2{(_Float16)-1032.0f, (_Float16)-1032.0f};
+    uint32_t r;
+    __builtin_memcpy(&r, &d, 4);
+    return r;
+}
+
 __global__ __launch_bounds__(256) void kvprep_kernel(const uint8_t *__restrict__ k, int64_t k_nb1, int64_t k_nb2,
                                                      const uint8_t *__restrict__ v, int64_t v_nb1, int64_t v_nb2,
                                                      int64_t n_kv, int64_t kv_tiles, uint8_t *__restrict__ kv,
@@ -159,17 +188,19 @@ __global__ __launch_bounds__(256) void kvprep_kernel(const uint8_t *__restrict__
         const int idx = t + 256 * i;
         const int key = idx >> 3, b = idx & 7;
         const uint16_t *src = reinterpret_cast<const uint16_t *>(sk + kHeadRowBytes * key + 18 * b);
-        uint16_t out[32];
+        // the block's 16 qs bytes as 4 dwords (they start 2 bytes off a dword for
+        // even b); codes 2j, 2j+1 (low nibbles) and 16 + 2j, 17 + 2j (high) as fp16
+        uint32_t q[4];
+        qs_dwords(sk + kHeadRowBytes * key, 18 * b + 2, q);
+        uint32_t out[16];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t two = src[1 + j];  // qs[2j], qs[2j+1]
-            const int b0 = two & 0xff, b1 = two >> 8;
-            const _Float16 c0 = (_Float16)((b0 & 15) - 8), c1 = (_Float16)((b1 & 15) - 8);
-            const _Float16 c2 = (_Float16)((b0 >> 4) - 8), c3 = (_Float16)((b1 >> 4) - 8);
-            __builtin_memcpy(&out[2 * j], &c0, 2);
-            __builtin_memcpy(&out[2 * j + 1], &c1, 2);
-            __builtin_memcpy(&out[16 + 2 * j], &c2, 2);
-            __builtin_memcpy(&out[16 + 2 * j + 1], &c3, 2);
+        for (int m = 0; m < 4; ++m) {
+            const uint32_t x0 = __builtin_amdgcn_perm(0u, q[m], 0x0c010c00u);  // bytes 4m, 4m+1
+            const uint32_t x1 = __builtin_amdgcn_perm(0u, q[m], 0x0c030c02u);  // bytes 4m+2, 4m+3
+            out[2 * m] = codes_f16(x0);
+            out[2 * m + 1] = codes_f16(x1);
+            out[8 + 2 * m] = codes_f16(x0 >> 4);
+            out[8 + 2 * m + 1] = codes_f16(x1 >> 4);
         }
         const int64_t gkey = k0 + key;
         const int r = key_row((int)(gkey & (kPK - 1)));
@@ -178,33 +209,44 @@ __global__ __launch_bounds__(256) void kvprep_kernel(const uint8_t *__restrict__
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int pos = (4 * b + j) ^ (r & 7);
-            uint4 x;
-            __builtin_memcpy(&x, out + 8 * j, 16);
+            const uint4 x = make_uint4(out[4 * j], out[4 * j + 1], out[4 * j + 2], out[4 * j + 3]);
             *reinterpret_cast<uint4 *>(row + 16 * pos) = swap_halves(x, r & 8);
         }
         *reinterpret_cast<uint16_t *>(rec + kOffDk + (b * kPK + r) * 2) = src[0];
     }
-    // V: thread t writes the Vc row of dim t (its 32 keys' codes, 64 bytes) of
-    // both tiles; threads 0..15 also write the Dv row of (tile t / 8, block t % 8)
+    // V: thread t takes dword m of block beta's qs (dims 32 beta + 4m + i from the
+    // low nibbles, 32 beta + 16 + 4m + i from the high ones, i < 4) for the 8 keys
+    // 8 kg .. 8 kg + 7 and writes those keys' 16-byte chunk of each of its 8 Vc
+    // rows (tile kg >> 2, chunk kg & 3); threads 0..15 also write the Dv row of
+    // (tile t / 8, block t % 8)
     {
-        const int d = t, beta = d >> 5, e = d & 31;
-        const int boff = 18 * beta + 2 + (e & 15), shift = 4 * (e >> 4);
+        const int beta = (t >> 2) & 7, m = t & 3, kg = t >> 5;
+        uint32_t w[8];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            uint16_t codes[32];
+        for (int kk = 0; kk < 8; ++kk) {
+            uint32_t q1[1];
+            qs_dwords<1>(sv + kHeadRowBytes * (8 * kg + kk), 18 * beta + 2 + 4 * m, q1);
+            w[kk] = q1[0];
+        }
+        uint8_t *vrec = kv + ((int64_t)h * kv_tiles + ((k0 >> 5) + (kg >> 2))) * kTileBytes + kKHalf;
+        const int c = kg & 3;  // keys 8c..8c+7 of the tile
 #pragma unroll
-            for (int kk = 0; kk < 32; ++kk) {
-                const int nib = (sv[kHeadRowBytes * (32 * u + kk) + boff] >> shift) & 15;
-                const _Float16 cv = (_Float16)(nib - 8);
-                __builtin_memcpy(&codes[kk], &cv, 2);
+        for (int i = 0; i < 4; ++i) {
+            // byte i of keys 2j (bits 0-7) and 2j + 1 (bits 16-23)
+            const uint32_t sel = (uint32_t)i | 0x0c00u | ((uint32_t)(4 + i) << 16) | 0x0c000000u;
+            uint32_t lo[4], hi[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t x = __builtin_amdgcn_perm(w[2 * j + 1], w[2 * j], sel);
+                lo[j] = codes_f16(x);
+                hi[j] = codes_f16(x >> 4);
             }
-            uint8_t *vrec = kv + ((int64_t)h * kv_tiles + ((k0 >> 5) + u)) * kTileBytes + kKHalf;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {  // keys 8c..8c+7 at chunk c ^ ((d >> 1) & 3), halves swapped when d & 8
-                uint4 x;
-                __builtin_memcpy(&x, codes + 8 * c, 16);
-                *reinterpret_cast<uint4 *>(vrec + 64 * d + 16 * (c ^ ((d >> 1) & 3))) = swap_halves(x, d & 8);
-            }
+            // chunk c of dim d at c ^ ((d >> 1) & 3), halves swapped when d & 8
+            const int dl = 32 * beta + 4 * m + i, dh = dl + 16;
+            *reinterpret_cast<uint4 *>(vrec + 64 * dl + 16 * (c ^ ((dl >> 1) & 3))) =
+                swap_halves(make_uint4(lo[0], lo[1], lo[2], lo[3]), dl & 8);
+            *reinterpret_cast<uint4 *>(vrec + 64 * dh + 16 * (c ^ ((dh >> 1) & 3))) =
+                swap_halves(make_uint4(hi[0], hi[1], hi[2], hi[3]), dh & 8);
         }
         uint32_t dmax = 0;
         if (t < 16) {
