@@ -217,8 +217,8 @@ __global__ __launch_bounds__(256) void kvprep_kernel(const uint8_t *__restrict__
     // V: thread t takes dword m of block beta's qs (dims 32 beta + 4m + i from the
     // low nibbles, 32 beta + 16 + 4m + i from the high ones, i < 4) for the 8 keys
     // 8 kg .. 8 kg + 7 and writes those keys' 16-byte chunk of each of its 8 Vc
-    // rows (tile kg >> 2, chunk kg & 3); threads 0..15 also write the Dv row of
-    // (tile t / 8, block t % 8)
+    // rows (tile kg >> 2, chunk kg & 3); the first wavefront also writes the Dv
+    // rows (below)
     {
         const int beta = (t >> 2) & 7, m = t & 3, kg = t >> 5;
         uint32_t w[8];
@@ -248,13 +248,14 @@ __global__ __launch_bounds__(256) void kvprep_kernel(const uint8_t *__restrict__
             *reinterpret_cast<uint4 *>(vrec + 64 * dh + 16 * (c ^ ((dh >> 1) & 3))) =
                 swap_halves(make_uint4(hi[0], hi[1], hi[2], hi[3]), dh & 8);
         }
+        // Dv rows: thread t < 64 takes tile u, block b, keys 8q..8q+7 of the tile
         uint32_t dmax = 0;
-        if (t < 16) {
-            const int u = t >> 3, b = t & 7;
-            uint16_t dd[32];
+        if (t < 64) {
+            const int u = t >> 5, b = (t >> 2) & 7, q = t & 3;
+            uint16_t dd[8];
 #pragma unroll
-            for (int kk = 0; kk < 32; ++kk) {
-                dd[kk] = *reinterpret_cast<const uint16_t *>(sv + kHeadRowBytes * (32 * u + kk) + 18 * b);
+            for (int kk = 0; kk < 8; ++kk) {
+                dd[kk] = *reinterpret_cast<const uint16_t *>(sv + kHeadRowBytes * (32 * u + 8 * q + kk) + 18 * b);
                 // a NaN/Inf scale (bytes that are not q4_0) reads as 0: such a key, if
                 // masked, adds exactly 0 (P d_v is formed in fp16, where 0 * NaN = NaN)
                 dd[kk] = (dd[kk] & 0x7C00u) == 0x7C00u ? (uint16_t)0 : dd[kk];
@@ -262,12 +263,9 @@ __global__ __launch_bounds__(256) void kvprep_kernel(const uint8_t *__restrict__
                 dmax = mag > dmax ? mag : dmax;
             }
             uint8_t *vrec = kv + ((int64_t)h * kv_tiles + ((k0 >> 5) + u)) * kTileBytes + kKHalf;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                uint4 x;
-                __builtin_memcpy(&x, dd + 8 * c, 16);
-                *reinterpret_cast<uint4 *>(vrec + kOffDv + 64 * b + 16 * c) = x;
-            }
+            uint4 x;
+            __builtin_memcpy(&x, dd, 16);
+            *reinterpret_cast<uint4 *>(vrec + kOffDv + 64 * b + 16 * q) = x;
         }
         if (t < 64) {
 #pragma unroll
