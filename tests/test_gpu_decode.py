@@ -78,11 +78,13 @@ def test_decode_kernel_other_group_sizes(sqa, orc, dev, H, n_q, n_kv):
 
 
 @pytest.mark.parametrize("Hkv,H,n_q,n_kv", [(1, 16, 1, 3000), (1, 8, 2, 70000), (4, 16, 2, 20000),
-                                            (8, 16, 1, 5000), (8, 32, 4, 1500), (16, 16, 1, 999)])
+                                            (8, 16, 1, 5000), (8, 32, 4, 1500), (16, 16, 1, 999),
+                                            (3, 12, 1, 40000), (6, 12, 2, 9000)])
 def test_decode_kernel_other_kv_head_counts(sqa, orc, dev, Hkv, H, n_q, n_kv):
     """Any number of KV heads: cache rows of Hkv x 144 bytes, G = H/Hkv query
     heads per KV head, splits scaled to about two workgroups per CU (capped at
-    256 splits for one KV head, 32 splits at 16 KV heads)."""
+    256 splits for one KV head, 32 splits at 16 KV heads; odd counts exercise
+    the workgroup-id division)."""
     q, kq, vq = qkv(orc, 57 + Hkv + H + n_q, n_q, n_kv, H=H, Hkv=Hkv, outliers=3)
     mask = orc.causal_mask(n_q, n_kv, n_kv - n_q)
     ref = orc.flash_attn_ext(q, kq, vq, mask)
