@@ -332,21 +332,8 @@ constexpr int kG2WAhead = 1;                  // weight super-blocks in flight a
 constexpr int kG2XBufs = kG2XAhead + 1;
 constexpr int kG2WBufs = kG2WAhead + 1;
 static_assert(2 * kG2WAhead >= kG2XAhead, "a weight stage is issued no later than the activations of its first half");
+static_assert(kG2XAhead == 1, "the per-half wait drains every DMA: the activations of the next half are issued last");
 static_assert(kG2WBytes % 1024 == 0, "weight stage in whole DMA instructions");
-
-// Wait until at most n vector-memory loads of this wavefront are outstanding and
-// its LDS accesses are done, then synchronise the workgroup (n wave-uniform).
-__device__ __forceinline__ void wait_vm_barrier(int n) {
-    switch (__builtin_amdgcn_readfirstlane(n)) {
-#define SQA_WAIT_CASE(N) \
-    case N: asm volatile("s_waitcnt vmcnt(" #N ") lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
-        SQA_WAIT_CASE(0) SQA_WAIT_CASE(1) SQA_WAIT_CASE(2) SQA_WAIT_CASE(3) SQA_WAIT_CASE(4)
-        SQA_WAIT_CASE(5) SQA_WAIT_CASE(6) SQA_WAIT_CASE(7) SQA_WAIT_CASE(8) SQA_WAIT_CASE(9)
-        SQA_WAIT_CASE(10) SQA_WAIT_CASE(11) SQA_WAIT_CASE(12) SQA_WAIT_CASE(13) SQA_WAIT_CASE(14)
-#undef SQA_WAIT_CASE
-        default: asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); break;
-    }
-}
 
 // 16 bytes per lane from sbase + voff into LDS at m0 + 16 * lane, asynchronously
 // (the caller waits with s_waitcnt vmcnt); sbase and m0 are wave-uniform.
@@ -456,23 +443,6 @@ __global__ __launch_bounds__(64 * kG2Waves) void op_gemm2_kernel(Gemm2Params p) 
     // the wait for activation half h, and every DMA it needs was issued no later
     // than that half's.
     const int nh = 2 * nsb, ngrp = (nsb + 3) / 4;
-    const int n_w = (kG2WPer - 1) * kG2Waves + wave < kG2WInst ? kG2WPer : kG2WPer - 1;  // weight DMAs per stage
-    const int n_s = wave < kG2Tok / 8 ? 1 : 0;
-    auto issued_in_half = [&](int k) -> int {
-        int c = 0;
-        if ((k & 1) == 0 && (k >> 1) + kG2WAhead < nsb) c += n_w;
-        if ((k & 7) == 0 && (k >> 3) + 1 < ngrp) c += n_s;
-        if (k + kG2XAhead < nh) c += kG2XInst;
-        return c;
-    };
-    // this wavefront's DMAs issued after activation half h
-    auto younger_than = [&](int h) -> int {
-        const int k0 = h - kG2XAhead;
-        int y = 0;
-        if (k0 < 0) y += ((nh < kG2XAhead ? nh : kG2XAhead) - 1 - h) * kG2XInst;  // later prologue halves
-        for (int k = k0 + 1 > 0 ? k0 + 1 : 0; k < h; ++k) y += issued_in_half(k);
-        return y;
-    };
     for (int sb = 0; sb < kG2WAhead && sb < nsb; ++sb) issue_w(sb, sb);
     issue_s(0);
     for (int k = 0; k < kG2XAhead && k < nh; ++k) issue_x(k, k);
@@ -490,8 +460,10 @@ __global__ __launch_bounds__(64 * kG2Waves) void op_gemm2_kernel(Gemm2Params p) 
         for (int hh = 0; hh < 2; ++hh) {
             const int h = 2 * sb + hh;
             // this wavefront's DMAs for half h have landed; the barrier publishes
-            // every wavefront's and retires the buffers the next DMAs overwrite
-            wait_vm_barrier(younger_than(h));
+            // every wavefront's and retires the buffers the next DMAs overwrite.
+            // Half h's activations were the last DMA issued (at the start of half
+            // h - 1, after that half's weights and S slots), so the wait drains all.
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
             if (hh == 0 && sb + kG2WAhead < nsb) issue_w(sb + kG2WAhead, (sb + kG2WAhead) % kG2WBufs);
             if (hh == 0 && u == 0 && (sb >> 2) + 1 < ngrp) issue_s((sb >> 2) + 1);
             if (h + kG2XAhead < nh) issue_x(h + kG2XAhead, (h + kG2XAhead) % kG2XBufs);
