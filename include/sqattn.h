@@ -243,11 +243,16 @@ int sqa_fill_causal_mask(const sqa_tensor *mask, int64_t step_start, void *strea
  *   x    F32  [K, M]  the attention output of M tokens (unit element stride)
  *   gate F32  [K, M]  or NULL (then dst = W . x)
  *   dst  F32  [N, M]  16-byte aligned rows
- * The weights enter as exact codes and (scale, min) pairs; the gated
- * activations as an fp16 hi + lo pair (about 22 bits, so |x| must stay below
- * 65504); products accumulate in fp32. ggml's CPU path instead rounds the
- * activations to 8 bits (its q8_K vec_dot type): this result is the closer of
- * the two to the exact W . x.
+ * The weights enter as exact codes and (scale, min) pairs; products
+ * accumulate in fp32. The gated activations xg = x * sigmoid(gate):
+ *   up to 4 tokens: fp32 throughout, any finite size;
+ *   more tokens: an fp16 hi + lo pair. Each value is carried to about 22 bits
+ *     where |xg| >= 2^-3 and to an absolute 2^-25 below that (the fp16
+ *     subnormal spacing of the lo part), so activations of RMS >= 1e-2 keep
+ *     the result within 1e-4 of its RMS; |xg| < 65504, and above 64 tokens
+ *     every 32-value sum of xg (a Q4_K sub-block) must also stay below 65504.
+ * ggml's CPU path instead rounds the activations to 8 bits (its q8_K vec_dot
+ * type): this result is the closer of the two to the exact W . x.
  */
 size_t sqa_out_proj_workspace_size(const sqa_tensor *w, const sqa_tensor *x);
 int sqa_supports_out_proj(const sqa_tensor *w, const sqa_tensor *x, const sqa_tensor *gate,

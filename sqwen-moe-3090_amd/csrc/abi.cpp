@@ -317,7 +317,8 @@ int sqa_flash_attn_ext_static(const sqa_tensor *q, const sqa_tensor *k, const sq
         return set_error(SQA_ERR_UNSUPPORTED,
                          "flash_attn_ext_static: only decode/verify shapes (up to 4 positions and 16 query "
                          "rows per KV head, 16-byte aligned q rows); use sqa_flash_attn_ext");
-    const size_t need = fa_decode_workspace(q->ne[1], q->ne[2], k->ne[2], k->ne[1]);
+    const size_t need = fa_decode_workspace(q->ne[1], q->ne[2], k->ne[2], k->ne[1],
+                                            decode_mask_needs_copy(mask, k->ne[1]));
     if (need > kStaticScratchBytes)
         return set_error(SQA_ERR_WORKSPACE,
                          "flash_attn_ext_static: these shapes need %zu bytes of scratch, above its %zu-byte "

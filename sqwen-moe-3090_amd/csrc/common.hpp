@@ -46,7 +46,10 @@ struct FaArgs {
     void *ws;
     size_t ws_bytes;
 };
-size_t fa_decode_workspace(int64_t n_q, int64_t H, int64_t n_kvh, int64_t n_kv);
+// Decode workspace bytes; mask_copy: the F16 mask needs the packed copy (its
+// rows are not 16-byte aligned or n_kv % 8 != 0, see decode_mask_needs_copy).
+size_t fa_decode_workspace(int64_t n_q, int64_t H, int64_t n_kvh, int64_t n_kv, bool mask_copy = true);
+bool decode_mask_needs_copy(const sqa_tensor *mask, int64_t n_kv);
 // Device scratch of the allocation-free decode entry point: its size, and its
 // address on the current device (looked up once per device).
 constexpr size_t kStaticScratchBytes = SQA_STATIC_SCRATCH_BYTES;

@@ -135,7 +135,8 @@ __device__ __forceinline__ void dma16(uint32_t voff, const void *sbase, uint32_t
     const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(b >> 32)) << 32) |
                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
     const uint32_t ms = (uint32_t)__builtin_amdgcn_readfirstlane((int)m0v);
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(bs), "s"(ms) : "memory");
+    // m0 as an operand: the compiler writes it and knows it holds the LDS base
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(bs), "{m0}"(ms) : "memory");
 }
 
 typedef const __attribute__((address_space(3))) uint32_t lds_u32;  // LDS dword from a raw LDS address
@@ -1035,12 +1036,16 @@ int static_scratch(void **out) {
     return SQA_OK;
 }
 
-size_t fa_decode_workspace(int64_t n_q, int64_t H, int64_t n_kvh, int64_t n_kv) {
+size_t fa_decode_workspace(int64_t n_q, int64_t H, int64_t n_kvh, int64_t n_kv, bool mask_copy) {
     const int64_t splits = decode_splits(n_kv, n_kvh);
     const size_t acc = al256((size_t)(splits * n_q * H * 256) * sizeof(float));
     const size_t ml = al256((size_t)(splits * n_q * H * 2) * sizeof(float));
-    const size_t mask = al256((size_t)(n_q * ((n_kv + 7) / 8 * 8)) * 2);
+    const size_t mask = mask_copy ? al256((size_t)(n_q * ((n_kv + 7) / 8 * 8)) * 2) : 0;
     return acc + ml + mask + 256;
+}
+
+bool decode_mask_needs_copy(const sqa_tensor *mask, int64_t n_kv) {
+    return mask && !((uintptr_t)mask->data % 16 == 0 && mask->nb[1] % 16 == 0 && n_kv % 8 == 0);
 }
 
 int launch_fa_decode(const FaArgs &a, hipStream_t s) {
@@ -1076,7 +1081,8 @@ int launch_fa_decode(const FaArgs &a, hipStream_t s) {
     p.w_first = p.n_first < p.n_splits ? kFirstRoundWeight : 1;
     p.w_second = p.n_first < p.n_splits ? kSecondRoundWeight : 1;
     p.cw_total = (int64_t)p.w_first * p.n_first + (int64_t)p.w_second * (p.n_splits - p.n_first);
-    const size_t need = fa_decode_workspace(n_q, H, Hkv, n_kv);
+    const bool pack_mask = a.q_pos0 < 0 && decode_mask_needs_copy(a.mask, n_kv);
+    const size_t need = fa_decode_workspace(n_q, H, Hkv, n_kv, pack_mask);
     if (!a.ws || a.ws_bytes < need)
         return set_error(SQA_ERR_WORKSPACE, "flash_attn_ext: workspace %zu bytes < %zu needed", a.ws_bytes, need);
     uint8_t *wsb = reinterpret_cast<uint8_t *>(((uintptr_t)a.ws + 255) & ~(uintptr_t)255);
@@ -1090,7 +1096,7 @@ int launch_fa_decode(const FaArgs &a, hipStream_t s) {
     if (a.q_pos0 < 0 && a.mask) {
         const char *m = (const char *)a.mask->data;
         const int64_t nb1 = (int64_t)a.mask->nb[1];
-        if ((uintptr_t)m % 16 == 0 && nb1 % 16 == 0 && n_kv % 8 == 0) {
+        if (!pack_mask) {
             p.mask = m;
             p.mask_nb1 = nb1;
             p.mask_len = n_kv;

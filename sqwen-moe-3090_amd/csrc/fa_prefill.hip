@@ -353,8 +353,8 @@ __global__ __launch_bounds__(256) void pf_mask_pack_kernel(const char *__restric
 // 16 bytes per lane from sbase + voff into LDS at m0 + 16 * lane (asynchronous;
 // the caller waits with s_waitcnt vmcnt).
 __device__ __forceinline__ void dma16(uint32_t voff, const void *sbase, uint32_t m0v) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(m0v)
-                 : "memory");
+    // m0 as an operand: the compiler writes it and knows it holds the LDS base
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0v) : "memory");
 }
 
 // Two 8-byte LDS reads into one MFMA operand. volatile keeps them two single

@@ -342,7 +342,8 @@ __device__ __forceinline__ void dma16(uint32_t voff, const void *sbase, uint32_t
     const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(b >> 32)) << 32) |
                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
     const uint32_t ms = (uint32_t)__builtin_amdgcn_readfirstlane((int)m0v);
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(bs), "s"(ms) : "memory");
+    // m0 as an operand: the compiler writes it and knows it holds the LDS base
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(bs), "{m0}"(ms) : "memory");
 }
 
 struct Gemm2Params {

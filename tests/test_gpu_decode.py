@@ -195,3 +195,31 @@ def test_masked_rows_with_garbage_bytes(sqa, orc, dev, n_q):
     got = run_gpu(sqa, dev, q, kq, vq, mask)
     assert np.all(np.isfinite(got))
     assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("Hkv,H,n_q,n_kv", [(2, 16, 1, 70000), (2, 16, 2, 9000), (1, 16, 1, 3000),
+                                           (8, 16, 2, 20000), (3, 24, 1, 777)])
+def test_workspace_garbage_and_reuse(sqa, orc, dev, Hkv, H, n_q, n_kv):
+    """The workspace is scratch the library fully rewrites: one workspace filled
+    with 0xFF bytes (NaN partials) serves four calls in a row, each of which
+    must match the oracle and give the same bytes. Shapes cover 1, 3 and 8 KV
+    heads and the minimum split count at short n_kv."""
+    q, kq, vq = qkv(orc, 900 + n_kv, n_q, n_kv, H=H, Hkv=Hkv)
+    mask = orc.causal_mask(n_q, n_kv, n_kv - n_q)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    qt = torch.from_numpy(q).to(dev)
+    kt = torch.from_numpy(np.ascontiguousarray(kq)).to(dev)
+    vt = torch.from_numpy(np.ascontiguousarray(vq)).to(dev)
+    mt = torch.from_numpy(mask).to(dev)
+    ws = torch.full((sqa.flash_attn_workspace_size(qt, kt, n_kv),), 0xFF, dtype=torch.uint8, device=dev)
+    first = None
+    for call in range(4):
+        out = torch.full((n_q, H, 256), float("nan"), device=dev)
+        sqa.flash_attn_ext(qt, kt, vt, n_kv, mask=mt, out=out, workspace=ws)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert np.all(np.isfinite(got)), call
+        assert rel_err(got, ref) <= TOL, call
+        if first is None:
+            first = got
+        assert np.array_equal(got, first), call

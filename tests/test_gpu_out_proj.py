@@ -32,30 +32,45 @@ def rel_max(got, ref):
     return float(np.abs(np.asarray(got, np.float64) - ref).max() / np.sqrt(np.mean(ref ** 2)))
 
 
-def run(sqa, orc, dev, N, K, M, seed, gate=True, outliers=0):
+def _offset_view(a, dev):
+    """The rows of a at a 4-byte offset from a 16-byte aligned allocation (and a
+    row stride of K + 1 floats): the kernels' scalar-load paths."""
+    M, K = a.shape
+    buf = torch.zeros((M, K + 1), dtype=torch.float32, device=dev)
+    buf[:, 1:] = torch.from_numpy(a).to(dev)
+    v = buf[:, 1:]
+    assert v.data_ptr() % 16 == 4
+    return v
+
+
+def run(sqa, orc, dev, N, K, M, seed, gate=True, outliers=0, scale=1.0, unaligned=False):
     rng = np.random.default_rng(seed)
     w = random_q4k(rng, N, K)
-    x = rng.standard_normal((M, K)).astype(np.float32)
+    x = rng.standard_normal((M, K)).astype(np.float32) * np.float32(scale)
     if outliers:
         x[:, rng.choice(K, outliers, replace=False)] *= 8
     g = rng.standard_normal((M, K)).astype(np.float32) if gate else None
     ref = orc.out_proj(w, x, g)
     wt = torch.from_numpy(w).to(dev)
-    xt = torch.from_numpy(x).to(dev)
-    gt = torch.from_numpy(g).to(dev) if gate else None
+    if unaligned:
+        xt = _offset_view(x, dev)
+        gt = _offset_view(g, dev) if gate else None
+    else:
+        xt = torch.from_numpy(x).to(dev)
+        gt = torch.from_numpy(g).to(dev) if gate else None
     out = sqa.out_proj(wt, xt, gt)
     torch.cuda.synchronize()
     err = rel_max(out.cpu().numpy(), ref)
-    print(f"out_proj N={N} K={K} M={M} gate={gate}: max err / rms = {err:.3e}")
+    print(f"out_proj N={N} K={K} M={M} gate={gate} scale={scale} unaligned={unaligned}: max err / rms = {err:.3e}")
     return err
 
 
-@pytest.mark.parametrize("M", [1, 2, 13, 16, 17, 64, 100, 512])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 13, 16, 17, 64, 100, 512])
 def test_out_proj_gated_n_embd_2048(sqa, orc, dev, M):
     assert run(sqa, orc, dev, 2048, 4096, M, 100 + M, outliers=8) <= TOL
 
 
-@pytest.mark.parametrize("M", [1, 40])
+@pytest.mark.parametrize("M", [1, 3, 4, 40])
 def test_out_proj_without_gate(sqa, orc, dev, M):
     assert run(sqa, orc, dev, 512, 4096, M, 200 + M, gate=False) <= TOL
 
@@ -67,6 +82,22 @@ def test_out_proj_small_and_ragged_shapes(sqa, orc, dev, N, K, M):
     # or 5 super-blocks (a partial group of four for the min term), token counts
     # that are not a multiple of 32
     assert run(sqa, orc, dev, N, K, M, 300 + N + M) <= TOL
+
+
+@pytest.mark.parametrize("M,gate", [(3, True), (3, False), (40, True), (1, True)])
+def test_out_proj_unaligned_activations(sqa, orc, dev, M, gate):
+    # x and gate rows 4 bytes off 16-byte alignment: the scalar-load forms of the
+    # decode kernel (M <= 4) and of the activation pass (M > 4)
+    assert run(sqa, orc, dev, 1024, 4096, M, 400 + M, gate=gate, unaligned=True) <= TOL
+
+
+@pytest.mark.parametrize("M,scale", [(1, 1e-4), (1, 3e3), (4, 1e-4), (4, 3e3), (17, 1e-2), (17, 1e3),
+                                     (512, 1e-2), (512, 1e3)])
+def test_out_proj_activation_scale(sqa, orc, dev, M, scale):
+    # up to 4 tokens the activations stay fp32 (any size); above, the fp16 hi + lo
+    # pair holds 1e-4 x RMS for activation RMS from 1e-2 up to 32-value sums
+    # below 65504 (1e3 x N(0,1) with 8x outlier channels)
+    assert run(sqa, orc, dev, 1024, 4096, M, 500 + M, outliers=8, scale=scale) <= TOL
 
 
 def test_out_proj_large_ubatch_without_gate(sqa, orc, dev):

@@ -2,7 +2,8 @@
 the workspace entry point (sqa_flash_attn_ext) through the C ABI: same kernels,
 so the outputs must be identical bit for bit. Two calls in a row, the second
 with a smaller input, so the second reuses scratch the first left behind; then
-its error paths (prefill shapes, scratch above its maximum)."""
+its error paths (prefill shapes, scratch above its maximum), and its use under
+HIP graph capture."""
 import numpy as np
 import pytest
 import torch
@@ -63,3 +64,41 @@ def test_static_entry_rejects_what_it_cannot_run(sqa, orc, dev):
     with pytest.raises(sqa.SqaError) as e:
         sqa.flash_attn_ext_static(qt, kt, kt, n_kv, mask=mt)
     assert e.value.status == 3 and "maximum" in str(e.value)
+
+
+def test_static_entry_graph_replay(sqa, orc, dev):
+    """The static entry captured once in a HIP graph (the use it exists for) with
+    an unaligned mask (n_kv odd: the packed copy runs inside the graph too) and
+    replayed at two positions, new Q and a new mask filled eagerly before each
+    replay; every replay is checked against the oracle."""
+    n_kv = 3001
+    _, kq, vq = qkv(orc, 71, 1, n_kv)
+    kt = torch.from_numpy(np.ascontiguousarray(kq)).to(dev)
+    vt = torch.from_numpy(np.ascontiguousarray(vq)).to(dev)
+    qt = torch.empty((1, 16, 256), device=dev)
+    mt = torch.empty((1, n_kv), dtype=torch.float16, device=dev)
+    out = torch.empty((1, 16, 256), device=dev)
+    rng = np.random.default_rng(72)
+    qt.copy_(torch.from_numpy(rng.standard_normal((1, 16, 256), dtype=np.float32)))
+    sqa.fill_causal_mask(mt, 2000)
+    sqa.flash_attn_ext_static(qt, kt, vt, n_kv, mask=mt, out=out)  # eager first call, outside the capture
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            sqa.flash_attn_ext_static(qt, kt, vt, n_kv, mask=mt, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for pos in (2500, 3000, 1234):
+        q = rng.standard_normal((1, 16, 256), dtype=np.float32)
+        qt.copy_(torch.from_numpy(q))
+        sqa.fill_causal_mask(mt, pos)
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        ref = orc.flash_attn_ext(q, kq, vq, orc.causal_mask(1, n_kv, pos))
+        err = rel_err(out.cpu().numpy(), ref)
+        print(f"static entry graph replay at position {pos}: max err / rms = {err:.3e}")
+        assert err <= 2e-3, pos
