@@ -84,12 +84,32 @@ def time_steps(torch, fn, steps):
     return a.elapsed_time(b)  # ms
 
 
+def capture(torch, fn):
+    """fn captured once in a HIP graph (on a side stream, after one eager call)."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    return g
+
+
 def verify_leg(sqa, torch, dev, ks, vs, steps):
     """MTP verify (n_q = 2: the current token plus one draft, causal across the
     two rows) against plain decode (n_q = 1) over the first n_kv rows of the 10
-    layers' caches, at 32768, 131072 and 172032 keys. The two step kinds
-    alternate within one loop, each bracketed by its own events, so the
-    marginal cost of the draft row is a difference of neighbouring steps."""
+    layers' caches, at 32768, 131072 and 172032 keys. Each 10-layer step is
+    captured in a HIP graph and replayed, so the figures are GPU time (at 32K a
+    layer takes less GPU time than the Python wrapper takes to launch it, and
+    eager launches would time the host); the two step kinds alternate within
+    one loop, each bracketed by its own events, so the marginal cost of the
+    draft row is a difference of neighbouring steps. Kernel times come from one
+    more eager pass with the library's event hooks; roofline = algorithmic
+    bytes / fa_decode time."""
     out = {}
     for n_kv in (32768, 131072, N_KV):
         q1 = torch.randn((1, H, D), device=dev)
@@ -107,30 +127,50 @@ def verify_leg(sqa, torch, dev, ks, vs, steps):
             for li in range(N_LAYERS):
                 sqa.flash_attn_ext(q, ks[li], vs[li], n_kv, mask=m, out=o, workspace=w)
 
+        run1 = lambda: run(q1, m1, o1, w1)
+        run2 = lambda: run(q2, m2, o2, w2)
+        g1, g2 = capture(torch, run1), capture(torch, run2)
         for _ in range(3):
-            run(q1, m1, o1, w1)
-            run(q2, m2, o2, w2)
+            g1.replay()
+            g2.replay()
         rounds = max(10, steps)
         ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(rounds)]
         torch.cuda.synchronize()
         for r in range(rounds):
             ev[r][0].record()
-            run(q1, m1, o1, w1)
+            g1.replay()
             ev[r][1].record()
-            run(q2, m2, o2, w2)
+            g2.replay()
             ev[r][2].record()
         torch.cuda.synchronize()
         t1 = sorted(e[0].elapsed_time(e[1]) for e in ev)
         t2 = sorted(e[1].elapsed_time(e[2]) for e in ev)
         marg = sorted(e[1].elapsed_time(e[2]) / e[0].elapsed_time(e[1]) - 1 for e in ev)
         med = lambda xs: xs[len(xs) // 2]
+        kern = {}
+        for name, fn in (("nq1", run1), ("nq2", run2)):
+            sqa.profile_begin(3 * N_LAYERS * 4 + 16)
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            sqa.profile_end()
+            for kn in ("fa_decode", "fa_combine"):
+                t, c = sqa.profile_get(kn)
+                if c:
+                    kern[f"{name}_{kn}"] = round(t / c * 1e3, 2)
+        frac = {name: round(layer_bytes(n_kv, nq) / (kern[f"{name}_fa_decode"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                for name, nq in (("nq1", 1), ("nq2", 2))}
         out[f"n_kv_{n_kv}"] = {
             "nq1_per_layer_us": round(med(t1) * 1e3 / N_LAYERS, 2),
             "nq2_per_layer_us": round(med(t2) * 1e3 / N_LAYERS, 2),
             "nq2_GB/s": round(N_LAYERS * layer_bytes(n_kv, 2) / (med(t2) * 1e-3) / 1e9, 1),
             "draft_row_marginal_pct": round(100 * med(marg), 1),
             "marginal_pct_iqr": [round(100 * marg[len(marg) // 4], 1), round(100 * marg[3 * len(marg) // 4], 1)],
+            "kernels_us": kern,
+            "fa_decode_roofline_frac": frac,
+            "timing": "HIP graph replay of the 10-layer step (GPU time); kernels from events, eager",
             "rounds": rounds}
+        del g1, g2
     return out
 
 
@@ -327,8 +367,16 @@ def out_proj_leg(sqa, torch, dev, np, steps, warmup):
         sqa.profile_end()
         tt, c = sqa.profile_get("out_proj")
         us = tt / c * 1e3
+        g = capture(torch, step)  # the same 10 layers without the Python launch cost
+        for _ in range(2):
+            g.replay()
+        ms_g = time_steps(torch, g.replay, steps) / steps
+        del g
+        gl = ms_g * 1e3 / N_LAYERS
         out[f"m{M}"] = {"per_layer_us": round(ms * 1e3 / N_LAYERS, 2), "kernels_us": round(us, 2),
+                        "graph_per_layer_us": round(gl, 2),
                         "weight_GB/s": round(w_bytes / (us * 1e-6) / 1e9, 1),
+                        "graph_weight_GB/s": round(w_bytes / (gl * 1e-6) / 1e9, 1),
                         "TFLOP/s": round(2 * N * K * M / (us * 1e-6) / 1e12, 2)}
     out["shape"] = {"K": K, "N": N, "weight": "Q4_K", "weight_bytes": w_bytes}
     return out

@@ -994,13 +994,20 @@ __global__ __launch_bounds__(256) void mask_pack_kernel(const char *__restrict__
 
 // About two workgroups per CU over all KV heads (one split per CU at 2 KV
 // heads), a multiple of 8 so that the workgroup numbering above holds (at most
-// kMaxSplits); at least ~4 tiles per split.
+// kMaxSplits); at least ~4 tiles per split, unless that leaves CUs idle: then
+// up to one workgroup per CU, down to one tile per split. Graph-replayed
+// 10-layer decode, us per layer (4-tile rule / this rule): 8K keys 13.3 /
+// 10.9, 16K 13.6 / 11.9; from 32K on the 4-tile rule already fills the CUs
+// (two workgroups per CU with 2-tile splits ran 16.4 against 14.0 at 32K).
 int decode_splits(int64_t n_kv, int64_t n_kvh) {
     const int64_t tiles = (n_kv + kTileKeys - 1) / kTileKeys;
-    int64_t cap = 2 * device_cu_count() / n_kvh / 8 * 8;
+    const int64_t cus = device_cu_count();
+    int64_t cap = 2 * cus / n_kvh / 8 * 8;
     if (cap > kMaxSplits) cap = kMaxSplits;
     if (cap < 8) cap = 8;
     int64_t s = (tiles + 3) / 4;
+    const int64_t fill = tiles < cus / n_kvh ? tiles : cus / n_kvh;  // one workgroup per CU
+    if (s < fill) s = fill;
     s = (s + 7) / 8 * 8;
     if (s > cap) s = cap;
     return (int)s;
