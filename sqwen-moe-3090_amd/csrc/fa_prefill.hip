@@ -282,10 +282,85 @@ __global__ __launch_bounds__(256) void kvprep_kernel(const uint8_t *__restrict__
 // q8_0 with ggml's x86 rounding (d = amax/127 over the block, codes =
 // rint(x * 127/amax)), then Q' = code * qd with qd = fp16(d) * scale * log2(e) in
 // fp32, written as fp16 hi = fp16(Q') and lo = fp16(Q' - hi).
+// Exclusive key limit of query tile `tile` under an F16 mask: 1 + the last
+// key any of its qb rows leaves visible (an entry other than -inf), 0 if none.
+// Keys past it are masked in every row of the tile, so the main kernel stops
+// there, as it does at the causal limit of the position form. Run by one
+// 256-thread workgroup: each wavefront takes 4 rows at a time and reads them
+// backwards 1024 keys per step (a lane takes two 8-key 16-byte loads per
+// row, all 8 loads in flight at once) until a step holds a visible key, so a
+// causal row costs its masked tail only: one step at pp512 (tails up to 511
+// keys), two for a 2048-token ubatch. Rows are 16-byte aligned with len (a
+// multiple of 8) readable keys. Every thread of the workgroup must call it.
+__device__ __forceinline__ void mask_tile_limit(const char *__restrict__ mask, int64_t nb1, int64_t len, int n_q, int qb, int tile,
+                                int32_t *__restrict__ lim) {
+    __shared__ int32_t best[4];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int q0 = tile * qb;
+    const int64_t c_top = (len - 1) / 1024 * 1024;
+    const uint4 none = make_uint4(0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u);
+    auto last_of = [&](uint4 a, uint4 b, int64_t c0) {  // the wavefront's last visible key in one step, or -1
+        int last = -1;
+        const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            if (((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) != 0xFC00u)
+                last = (int)(c0 + 512 * (e >> 3) + 8 * lane + (e & 7));
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) last = max(last, __shfl_xor(last, o));
+        return last;
+    };
+    auto load = [&](const uint16_t *row, int64_t k) {
+        return k < len ? *reinterpret_cast<const uint4 *>(row + k) : none;
+    };
+    int32_t mine = -1;  // wave-uniform
+    for (int r0 = 4 * wave; r0 < qb; r0 += 16) {
+        uint4 a[4], b[4];
+        const uint16_t *rows[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {  // the first step of four rows at once
+            const bool ok = r0 + j < qb && q0 + r0 + j < n_q;
+            rows[j] = ok ? reinterpret_cast<const uint16_t *>(mask + (int64_t)(q0 + r0 + j) * nb1) : nullptr;
+            a[j] = ok ? load(rows[j], c_top + 8 * lane) : none;
+            b[j] = ok ? load(rows[j], c_top + 512 + 8 * lane) : none;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int last = last_of(a[j], b[j], c_top);
+            for (int64_t c0 = c_top - 1024; last < 0 && rows[j] && c0 >= 0; c0 -= 1024)  // longer tails
+                last = last_of(load(rows[j], c0 + 8 * lane), load(rows[j], c0 + 512 + 8 * lane), c0);
+            mine = max(mine, last);
+        }
+    }
+    if (lane == 0) best[wave] = mine;
+    __syncthreads();
+    if (threadIdx.x == 0) lim[tile] = max(max(best[0], best[1]), max(best[2], best[3])) + 1;
+}
+
+// The same as a kernel of its own, for a packed mask copy (written after the
+// Q pre-pass): one workgroup per query tile.
+__global__ __launch_bounds__(256) void mask_tile_limit_kernel(const char *__restrict__ mask, int64_t nb1, int64_t len,
+                                                              int n_q, int qb, int32_t *__restrict__ lim) {
+    mask_tile_limit(mask, nb1, len, n_q, qb, blockIdx.x, lim);
+}
+
+// Workgroups from n_qblocks on are the mask scan (mask_tile_limit) of query
+// tile blockIdx.x - n_qblocks, when the kernel reads the caller's mask in place.
+struct MaskScan {
+    const char *mask;  // null: no scan here
+    int64_t nb1, len;
+    int qb, n_qblocks;
+    int32_t *lim;
+};
+
 __global__ __launch_bounds__(256) void qprep_kernel(const char *__restrict__ q, int64_t nb1, int64_t nb2,
                                                     int n_q, int H, float qscale, uint16_t *__restrict__ qh,
                                                     uint16_t *__restrict__ ql, uint32_t *__restrict__ dvmax, int hkv,
-                                                    bool aligned) {
+                                                    bool aligned, MaskScan ms) {
+    if (ms.mask && (int)blockIdx.x >= ms.n_qblocks) {
+        mask_tile_limit(ms.mask, ms.nb1, ms.len, n_q, ms.qb, (int)blockIdx.x - ms.n_qblocks, ms.lim);
+        return;
+    }
     // one thread per 8 values: a quad of lanes owns a 32-value block
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (gid < hkv) dvmax[gid] = 0;  // for kvprep_kernel, launched next
@@ -381,6 +456,7 @@ struct PrefillParams {
     const char *mask;  // F16 rows 16-byte aligned, mask_len (a multiple of 8) keys each, or null
     int64_t mask_nb1, mask_len;
     int64_t q_pos0;    // >= 0: causal from positions (mask ignored)
+    const int32_t *tile_lim;  // with a mask: [q_tiles] exclusive key limit of each query tile
     int n_splits;
     int q_tiles;        // workgroups per (KV head, split)
     int64_t split_len;  // keys per split, a multiple of kPK
@@ -417,6 +493,9 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
     if (p.q_pos0 >= 0) {
         const int64_t q_last = (q_base + p.qb < p.n_q ? q_base + p.qb : p.n_q) - 1;
         const int64_t lim = p.q_pos0 + q_last + 1;
+        if (k_end > lim) k_end = lim;
+    } else if (p.tile_lim) {  // the mask's last visible key over the tile's rows
+        const int64_t lim = p.tile_lim[q_tile];
         if (k_end > lim) k_end = lim;
     }
     const int n_tiles = k_end > k_begin ? (int)((k_end - k_begin + kPK - 1) / kPK) : 0;
@@ -850,7 +929,7 @@ struct PrefillPlan {
     int64_t kv_tiles;
     int qb, q_tiles, n_splits, mask_stage;
     int64_t split_len;
-    size_t off_kv, off_dvmax, off_qh, off_ql, off_mask, off_pa, off_pm, total;
+    size_t off_kv, off_dvmax, off_qh, off_ql, off_mask, off_lim, off_pa, off_pm, total;
 };
 
 PrefillPlan plan(int64_t n_q, int64_t H, int64_t Hkv, int64_t n_kv) {
@@ -875,6 +954,7 @@ PrefillPlan plan(int64_t n_q, int64_t H, int64_t Hkv, int64_t n_kv) {
     pl.off_qh = o; o = al256(o + (size_t)n_q * H * kHeadDim * 2);
     pl.off_ql = o; o = al256(o + (size_t)n_q * H * kHeadDim * 2);
     pl.off_mask = o; o = al256(o + (size_t)n_q * ((n_kv + 7) / 8 * 8) * 2);
+    pl.off_lim = o; o = al256(o + (size_t)pl.q_tiles * 4);
     pl.off_pa = o;
     pl.off_pm = o;
     if (pl.n_splits > 1) {
@@ -936,9 +1016,14 @@ int launch_fa_prefill(const FaArgs &a, hipStream_t s) {
     int prof = profile_start("fa_prefill_prep", s);
     {
         const int64_t nqb = n_q * H * kBlocksPerHead;
-        qprep_kernel<<<dim3((unsigned)((4 * nqb + 255) / 256)), dim3(256), 0, s>>>(
+        const int qblocks = (int)((4 * nqb + 255) / 256);
+        int32_t *lim = reinterpret_cast<int32_t *>(base + pl.off_lim);
+        // an in-place mask is scanned by extra workgroups of the Q pre-pass, a
+        // packed copy by a kernel of its own once it is written
+        const MaskScan ms{p.mask && !mask_src ? p.mask : nullptr, p.mask_nb1, p.mask_len, pl.qb, qblocks, lim};
+        qprep_kernel<<<dim3((unsigned)(qblocks + (ms.mask ? pl.q_tiles : 0))), dim3(256), 0, s>>>(
             (const char *)q.data, (int64_t)q.nb[1], (int64_t)q.nb[2], (int)n_q, (int)H, a.scale * kLog2e, qh, ql,
-            dvmax, (int)Hkv, (uintptr_t)q.data % 16 == 0 && q.nb[1] % 16 == 0 && q.nb[2] % 16 == 0);
+            dvmax, (int)Hkv, (uintptr_t)q.data % 16 == 0 && q.nb[1] % 16 == 0 && q.nb[2] % 16 == 0, ms);
         kvprep_kernel<<<dim3((unsigned)(pl.kv_tiles / 2), (unsigned)Hkv), dim3(256), 0, s>>>(
             (const uint8_t *)k.data, (int64_t)k.nb[1], (int64_t)k.nb[2], (const uint8_t *)v.data, (int64_t)v.nb[1],
             (int64_t)v.nb[2], n_kv, pl.kv_tiles, kv, dvmax);
@@ -948,11 +1033,15 @@ int launch_fa_prefill(const FaArgs &a, hipStream_t s) {
             pf_mask_pack_kernel<<<dim3((unsigned)grid), dim3(256), 0, s>>>(
                 mask_src, mask_src_nb1, n_kv, (int)n_q, p.mask_len, (uint16_t *)(base + pl.off_mask));
         }
+        if (mask_src)  // the packed copy, just written
+            mask_tile_limit_kernel<<<dim3((unsigned)pl.q_tiles), dim3(256), 0, s>>>(
+                p.mask, p.mask_nb1, p.mask_len, (int)n_q, pl.qb, reinterpret_cast<int32_t *>(base + pl.off_lim));
     }
     profile_stop(prof, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_status(e, "prefill pre-pass launch");
 
+    p.tile_lim = p.mask ? reinterpret_cast<const int32_t *>(base + pl.off_lim) : nullptr;
     p.kv = kv;
     p.dvmax = dvmax;
     p.qh = qh;

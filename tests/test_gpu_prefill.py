@@ -143,3 +143,82 @@ def test_prefill_masked_rows_with_garbage_bytes(sqa, orc, dev):
     got = run_gpu(sqa, dev, q, kq, vq, mask)
     assert np.all(np.isfinite(got))
     assert rel_err(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("n_q,n_kv,unaligned", [(200, 3000, False), (300, 1500, True), (64, 4096, False)])
+def test_prefill_mask_trim_with_irregular_masks(sqa, orc, dev, n_q, n_kv, unaligned):
+    """The mask path stops each query tile at the last key any of its rows
+    leaves visible. Rows here end their visible keys at random places (not a
+    causal staircase), some have -inf holes before that end, one row is fully
+    masked, and masked keys hold 0xFF bytes: the trimmed kernel must match the
+    oracle. unaligned: n_kv % 8 != 0 and an odd row stride (the packed copy is
+    what gets scanned)."""
+    if unaligned:
+        n_kv += 3
+    rng = np.random.default_rng(n_q + n_kv)
+    q, kq, vq = qkv(orc, 2000 + n_q, n_q, n_kv)
+    mask = np.zeros((n_q, n_kv), dtype=np.float16)
+    ends = rng.integers(1, n_kv + 1, n_q)
+    for r in range(n_q):
+        mask[r, ends[r]:] = -np.inf
+        holes = rng.choice(ends[r], min(ends[r] - 1, 5), replace=False) if ends[r] > 1 else []
+        mask[r, holes] = -np.inf
+    mask[n_q // 3] = -np.inf
+    kq, vq = kq.copy(), vq.copy()
+    dead = np.where(np.all(np.isinf(mask), axis=0))[0]
+    kq[dead] = 0xFF
+    vq[dead] = 0xFF
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    if unaligned:  # rows with a stride of n_kv + 1 halfs
+        buf = np.full((n_q, n_kv + 1), -np.inf, dtype=np.float16)
+        buf[:, :n_kv] = mask
+        qt = torch.from_numpy(q).to(dev)
+        kt = torch.from_numpy(np.ascontiguousarray(kq)).to(dev)
+        vt = torch.from_numpy(np.ascontiguousarray(vq)).to(dev)
+        mt = torch.from_numpy(buf).to(dev)[:, :n_kv]
+        got = sqa.flash_attn_ext(qt, kt, vt, n_kv, mask=mt, scale=1 / 16)
+        torch.cuda.synchronize()
+        got = got.cpu().numpy()
+    else:
+        got = run_gpu(sqa, dev, q, kq, vq, mask)
+    assert np.all(np.isfinite(got))
+    err = rel_err(got, ref)
+    print(f"irregular mask n_q={n_q} n_kv={n_kv}: max err / rms = {err:.3e}")
+    assert err <= TOL
+
+
+def test_mask_form_start_chunk_costs_what_the_causal_form_does(sqa, orc, dev):
+    """The first chunk of a prompt (512 queries at positions 0..511) through the
+    engine's F16 mask: half of its key tiles are masked in every row of their
+    query tile and must be skipped as the causal-from-positions form skips them.
+    Parity first, then the main kernel's time (HIP events, median of 7 rounds of
+    10 calls, the two forms alternating) within 10% of the causal form's."""
+    n_q = n_kv = 512
+    q, kq, vq = qkv(orc, 4242, n_q, n_kv, outliers=5)
+    mask = orc.causal_mask(n_q, n_kv, 0)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    qt = torch.from_numpy(q).to(dev)
+    kt = torch.from_numpy(np.ascontiguousarray(kq)).to(dev)
+    vt = torch.from_numpy(np.ascontiguousarray(vq)).to(dev)
+    mt = torch.from_numpy(mask).to(dev)
+    out = torch.empty((n_q, 16, 256), device=dev)
+    ws = torch.empty(sqa.flash_attn_workspace_size(qt, kt, n_kv), dtype=torch.uint8, device=dev)
+    sqa.flash_attn_ext(qt, kt, vt, n_kv, mask=mt, scale=1 / 16, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    assert rel_err(out.cpu().numpy(), ref) <= TOL
+    forms = {"mask": lambda: sqa.flash_attn_ext(qt, kt, vt, n_kv, mask=mt, scale=1 / 16, out=out, workspace=ws),
+             "causal": lambda: sqa.flash_attn_ext_causal(qt, kt, vt, n_kv, 0, scale=1 / 16, out=out, workspace=ws)}
+    times = {k: [] for k in forms}
+    for r in range(7):
+        for name in (("mask", "causal") if r % 2 == 0 else ("causal", "mask")):
+            sqa.profile_begin(64)
+            for _ in range(10):
+                forms[name]()
+            torch.cuda.synchronize()
+            sqa.profile_end()
+            t, c = sqa.profile_get("fa_prefill")
+            times[name].append(t / c)
+    med = {k: sorted(v)[len(v) // 2] for k, v in times.items()}
+    print(f"start chunk 512x512: fa_prefill mask form {1e3 * med['mask']:.2f} us, "
+          f"causal form {1e3 * med['causal']:.2f} us")
+    assert med["mask"] <= 1.10 * med["causal"]
