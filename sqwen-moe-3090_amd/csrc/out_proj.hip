@@ -42,8 +42,6 @@ constexpr int kQK = 256;           // values per Q4_K super-block
 constexpr int kBlockBytes = 144;   // bytes per super-block
 constexpr int kSubs = kQK / 32;    // sub-blocks per super-block
 constexpr int kGemvTokens = 4;     // token counts up to this take op_gemv
-constexpr int kGemvMaxLds = 160 * 1024;
-constexpr int kGemvSbStride = kQK + 4;  // floats per super-block of activations in LDS
 
 __device__ __forceinline__ float h2f(uint32_t bits) {
     _Float16 h;
@@ -605,171 +603,150 @@ __global__ __launch_bounds__(64 * kG2Waves) void op_gemm2_kernel(Gemm2Params p) 
 }
 
 // ---------------------------------------------------------------- op_gemv
-// Decode and verify (M <= 4 tokens, MT = 1, 2 or 4 slots): one workgroup of 256
-// threads takes 8 rows of W; thread (row, l32) takes half h = l32 & 1 (code
-// groups 2h, 2h+1) of super-blocks l32 / 2, l32 / 2 + 16, ... of its row, so a
-// row's bytes are read by 32 consecutive threads. The thread accumulates
-// sum(code * xg) and sum(xg) per sub-block: out += d*scale * sum(code * xg) -
-// dmin*min * sum(xg). Codes enter as fp16 subnormals (code * 2^-24, two per
-// v_and) into v_fma_mix with the fp32 activations, so every product is exact
-// and the 2^24 goes into the scale. The gated activations and their sub-block
-// sums are built in LDS by the workgroup itself (no separate pass), while the
-// thread's first weights are already in flight. VEC: x (and gate) rows are
-// 16-byte aligned and read four floats at a time.
+// Decode and verify (M <= 4 tokens, MT = 1, 2 or 4 slots): one workgroup of
+// kGemvThreads threads takes kGemvRows rows of W. Thread t owns the 8
+// activations k = 8t .. 8t + 7 (and the same slice of every further
+// 8 * kGemvThreads values of K) for all of those rows, so it loads its slice of
+// x and gate once and, for each row, the slice's 8 code bytes and the
+// super-block header, all before it uses any of them: one memory latency, then
+// arithmetic, then one reduction.
+//   Value 64j + 16h2 + i of a super-block sits in byte 32j + 16(h2 & 1) + i of
+//   its codes, low nibble for h2 < 2, high for h2 >= 2; sub-block 2j + (h2 >> 1).
+// Per row and token: out += d * scale * sum(code * xg) - dmin * min * sum(xg).
+// The codes enter v_fma_mix as fp16 subnormals, two per v_and, against the
+// fp32 activations, so every product is exact: a low nibble left in bits 0-3
+// of an fp16 is code * 2^-24, a high nibble left in bits 4-7 is code * 2^-20,
+// and the 2^24 or 2^20 goes into the scale. The gate's sigmoid is 1/(1 + 2^(-g
+// log2 e)) from the hardware exp2 and reciprocal (about 2 ulp). The partial
+// sums of each (row, token) are added by DPP row rotations and lane swaps
+// inside each wavefront, then across the wavefronts through LDS. VEC: x (and
+// gate) rows are 16-byte aligned and read four floats at a time.
+constexpr int kGemvRows = 8;
+constexpr int kGemvThreads = 512;
 template <int MT, bool VEC>
-__global__ __launch_bounds__(256) void op_gemv_kernel(const uint8_t *__restrict__ w, int64_t w_nb1,
-                                                      const char *__restrict__ x, int64_t x_nb1,
-                                                      const char *__restrict__ gate, int64_t g_nb1, int K, int N,
-                                                      int M, float *__restrict__ dst, int64_t d_nb1) {
-    // [MT][K/256][kGemvSbStride] gated activations (a super-block's 256 values
-    // padded to 260 floats, so the super-blocks a wavefront reads at once sit on
-    // different bank quads), then [MT][K/32] sub-block sums
-    extern __shared__ __align__(16) float xs[];
-    const int tid = threadIdx.x;
-    const int nsb = K / kQK;
-    const int tstride = nsb * kGemvSbStride;
-    float *ssum = xs + MT * tstride;
-    const int row = blockIdx.x * 8 + (tid >> 5), l32 = tid & 31, hj = l32 & 1;
-    const uint8_t *wr = w + (int64_t)row * w_nb1;
-    // header (d, dmin, scales) and the 64 code bytes of groups 2h, 2h+1
-    uint4 hdr, qb[4];
-    auto load_w = [&](int sb) {
-        const uint4 *blk = reinterpret_cast<const uint4 *>(wr + (int64_t)sb * kBlockBytes);
-        hdr = blk[0];
+__global__ __launch_bounds__(kGemvThreads) void op_gemv_kernel(const uint8_t *__restrict__ w, int64_t w_nb1,
+                                                               const char *__restrict__ x, int64_t x_nb1,
+                                                               const char *__restrict__ gate, int64_t g_nb1, int K,
+                                                               int N, int M, float *__restrict__ dst, int64_t d_nb1) {
+    constexpr int R = kGemvRows, W = kGemvThreads / 64;
+    __shared__ float red[W][R * MT];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row0 = blockIdx.x * R;
+    float acc[R][MT];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) qb[c] = blk[1 + 4 * hj + c];
-    };
-    if ((l32 >> 1) < nsb) load_w(l32 >> 1);  // in flight while the activations load
-    auto gated = [&](float v, float g) { return gate ? v * (1.0f / (1.0f + expf(-g))) : v; };
-    if (VEC) {
-        // 16 values per thread per round as four float4, all loads of a round
-        // issued before any use (K is a multiple of 256: a float4 stays in one token row)
-        for (int i0 = 0; i0 < MT * K; i0 += 256 * 16) {
-            float4 v[4], gv[4];
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int i = i0 + 4 * (256 * u + tid);
-                const int t = i / K, k = i - t * K;
-                const bool ok = i < MT * K && t < M;
-                v[u] = gv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (ok) {
-                    v[u] = *reinterpret_cast<const float4 *>(x + t * x_nb1 + 4 * (int64_t)k);
-                    if (gate) gv[u] = *reinterpret_cast<const float4 *>(gate + t * g_nb1 + 4 * (int64_t)k);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int i = i0 + 4 * (256 * u + tid);
-                const int t = i / K, k = i - t * K;
-                if (i < MT * K)
-                    *reinterpret_cast<float4 *>(xs + t * tstride + (k >> 8) * kGemvSbStride + (k & 255)) =
-                        make_float4(gated(v[u].x, gv[u].x), gated(v[u].y, gv[u].y), gated(v[u].z, gv[u].z),
-                                    gated(v[u].w, gv[u].w));
-            }
-        }
-    } else {
-        for (int i0 = 0; i0 < MT * K; i0 += 256 * 16) {
-            float v[16], gv[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const int i = i0 + 256 * u + tid;
-                const int t = i / K, k = i - t * K;
-                const bool ok = i < MT * K && t < M;
-                v[u] = ok ? reinterpret_cast<const float *>(x + t * x_nb1)[k] : 0.0f;
-                gv[u] = ok && gate ? reinterpret_cast<const float *>(gate + t * g_nb1)[k] : 0.0f;
-            }
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const int i = i0 + 256 * u + tid;
-                const int t = i / K, k = i - t * K;
-                if (i < MT * K) xs[t * tstride + (k >> 8) * kGemvSbStride + (k & 255)] = gated(v[u], gv[u]);
-            }
-        }
-    }
-    __syncthreads();
-    for (int i = tid; i < MT * (K / 32); i += 256) {
-        const int t = i / (K / 32), sub = i - t * (K / 32);
-        const float4 *src = reinterpret_cast<const float4 *>(xs + t * tstride + (sub >> 3) * kGemvSbStride + 32 * (sub & 7));
-        float a = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float4 f = src[j];
-            a += (f.x + f.y) + (f.z + f.w);
-        }
-        ssum[i] = a;
-    }
-    __syncthreads();
-    float acc[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
-    // x * (code 2^-24) + acc, the code in the low (SEL 0) or high (SEL 1) fp16 half of c
+        for (int t = 0; t < MT; ++t) acc[r][t] = 0.0f;
+    // x * code + acc, the code in the low (SEL 0) or high (SEL 1) fp16 half of c
 #define SQA_MIX(ACC, X, C, SEL)                                                                           \
     asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[0," #SEL ",0] op_sel_hi:[0,1,0]" : "+v"(ACC) : "v"(X), "v"(C))
-    for (int sb = l32 >> 1; sb < nsb; sb += 16) {
-        if (sb != (l32 >> 1)) load_w(sb);
-        const float d = h2f(hdr.x & 0xffffu), dmin = h2f(hdr.x >> 16);
+    for (int k0 = 8 * tid; k0 < K; k0 += 8 * kGemvThreads) {
+        const int sb = k0 >> 8, v = k0 & 255, j = v >> 6, h2 = (v >> 4) & 3;
+        const bool hi_nib = h2 >= 2;
+        const uint32_t nib = hi_nib ? 0x00F000F0u : 0x000F000Fu;  // codes of bytes 0, 2 of a dword
+        const float cscale = hi_nib ? 1048576.0f : 16777216.0f;     // 2^20 or 2^24
+        const int s = 2 * j + (h2 >> 1);                            // sub-block
+        const int cb = 16 + 32 * j + 16 * (h2 & 1) + (v & 8);       // the slice's first code byte
+        // weights of all rows first (header, 8 code bytes), then the activations
+        uint4 hdr[R];
+        uint2 q[R];
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-            const int j = 2 * hj + jj;  // sub-blocks 2j (low nibbles) and 2j+1 (high)
-            int sc0, mn0, sc1, mn1;
-            scale_min(hdr.y, hdr.z, hdr.w, 2 * j, sc0, mn0);
-            scale_min(hdr.y, hdr.z, hdr.w, 2 * j + 1, sc1, mn1);
-            float dl[MT], dh[MT];
+        for (int r = 0; r < R; ++r) {
+            const uint8_t *blk = w + (int64_t)(row0 + r) * w_nb1 + (int64_t)sb * kBlockBytes;
+            hdr[r] = *reinterpret_cast<const uint4 *>(blk);
+            q[r] = *reinterpret_cast<const uint2 *>(blk + cb);
+        }
+        float xg[MT][8];
 #pragma unroll
-            for (int t = 0; t < MT; ++t) dl[t] = dh[t] = 0.0f;
-            const float *xl = xs + sb * kGemvSbStride + 64 * j;
+        for (int t = 0; t < MT; ++t) {
+            const bool ok = t < M;
+            const float *xr = reinterpret_cast<const float *>(x + (ok ? t : 0) * x_nb1) + k0;
+            const float *gr = gate ? reinterpret_cast<const float *>(gate + (ok ? t : 0) * g_nb1) + k0 : nullptr;
+            float gv[8];
+            if (VEC) {
 #pragma unroll
-            for (int m = 0; m < 8; ++m) {
-                // code bytes 32j + 4m .. +3: dword m of the group's 32 bytes
-                const uint4 qv = qb[2 * jj + (m >> 2)];
-                const uint32_t q = (m & 3) == 0 ? qv.x : (m & 3) == 1 ? qv.y : (m & 3) == 2 ? qv.z : qv.w;
-                const uint32_t c02 = q & 0x000F000Fu;           // low nibbles of bytes 0, 2
-                const uint32_t c13 = (q >> 8) & 0x000F000Fu;    // of bytes 1, 3
-                const uint32_t h02 = (q >> 4) & 0x000F000Fu;    // high nibbles of bytes 0, 2
-                const uint32_t h13 = (q >> 12) & 0x000F000Fu;   // of bytes 1, 3
+                for (int c = 0; c < 2; ++c) {
+                    const float4 a = reinterpret_cast<const float4 *>(xr)[c];
+                    xg[t][4 * c] = a.x, xg[t][4 * c + 1] = a.y, xg[t][4 * c + 2] = a.z, xg[t][4 * c + 3] = a.w;
+                    if (gr) {
+                        const float4 b = reinterpret_cast<const float4 *>(gr)[c];
+                        gv[4 * c] = b.x, gv[4 * c + 1] = b.y, gv[4 * c + 2] = b.z, gv[4 * c + 3] = b.w;
+                    }
+                }
+            } else {
 #pragma unroll
-                for (int t = 0; t < MT; ++t) {
-                    const float4 xa = *reinterpret_cast<const float4 *>(xl + t * tstride + 4 * m);
-                    const float4 xb = *reinterpret_cast<const float4 *>(xl + t * tstride + 32 + 4 * m);
-                    SQA_MIX(dl[t], xa.x, c02, 0);
-                    SQA_MIX(dl[t], xa.y, c13, 0);
-                    SQA_MIX(dl[t], xa.z, c02, 1);
-                    SQA_MIX(dl[t], xa.w, c13, 1);
-                    SQA_MIX(dh[t], xb.x, h02, 0);
-                    SQA_MIX(dh[t], xb.y, h13, 0);
-                    SQA_MIX(dh[t], xb.z, h02, 1);
-                    SQA_MIX(dh[t], xb.w, h13, 1);
+                for (int i = 0; i < 8; ++i) {
+                    xg[t][i] = xr[i];
+                    if (gr) gv[i] = gr[i];
                 }
             }
-            const float s0 = d * (float)sc0 * 16777216.0f, m0 = dmin * (float)mn0;
-            const float s1 = d * (float)sc1 * 16777216.0f, m1 = dmin * (float)mn1;
 #pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                const float *st = ssum + t * (K / 32) + sb * kSubs + 2 * j;
-                float a = fmaf(s0, dl[t], acc[t]);
-                a = fmaf(-m0, st[0], a);
-                a = fmaf(s1, dh[t], a);
-                acc[t] = fmaf(-m1, st[1], a);
+            for (int i = 0; i < 8; ++i) {
+                if (gr)
+                    xg[t][i] *= __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * gv[i]));
+                xg[t][i] = ok ? xg[t][i] : 0.0f;
             }
+        }
+        float sx[MT];  // sum of this slice's activations (the min term)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+            sx[t] = ((xg[t][0] + xg[t][1]) + (xg[t][2] + xg[t][3])) + ((xg[t][4] + xg[t][5]) + (xg[t][6] + xg[t][7]));
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t qw[2] = {q[r].x, q[r].y};
+            float dot[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t) dot[t] = 0.0f;
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {  // bytes 4m .. 4m+3 of the slice: values 4m .. 4m+3
+                const uint32_t c02 = qw[m] & nib;         // values 4m, 4m + 2
+                const uint32_t c13 = (qw[m] >> 8) & nib;  // values 4m + 1, 4m + 3
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    SQA_MIX(dot[t], xg[t][4 * m], c02, 0);
+                    SQA_MIX(dot[t], xg[t][4 * m + 1], c13, 0);
+                    SQA_MIX(dot[t], xg[t][4 * m + 2], c02, 1);
+                    SQA_MIX(dot[t], xg[t][4 * m + 3], c13, 1);
+                }
+            }
+            // 6-bit scale and min of sub-block s (ggml's get_scale_min_k4), branch-free
+            const uint32_t q0 = hdr[r].y, q1 = hdr[r].z, q2 = hdr[r].w;
+            const uint32_t lo_sh = 8u * (uint32_t)(s & 3);
+            const uint32_t sc_lo = (q0 >> lo_sh) & 63u, mn_lo = (q1 >> lo_sh) & 63u;
+            const uint32_t sc_hi = ((q2 >> lo_sh) & 15u) | (((q0 >> (lo_sh + 6u)) & 3u) << 4);
+            const uint32_t mn_hi = ((q2 >> (lo_sh + 4u)) & 15u) | (((q1 >> (lo_sh + 6u)) & 3u) << 4);
+            const uint32_t sc = s < 4 ? sc_lo : sc_hi, mn = s < 4 ? mn_lo : mn_hi;
+            const float ds = h2f(hdr[r].x & 0xffffu) * (float)sc * cscale;
+            const float dm = h2f(hdr[r].x >> 16) * (float)mn;
+#pragma unroll
+            for (int t = 0; t < MT; ++t) acc[r][t] = fmaf(-dm, sx[t], fmaf(ds, dot[t], acc[r][t]));
         }
     }
 #undef SQA_MIX
-    // the 32 threads of a row are 32 consecutive lanes: DPP rotations inside each
-    // 16-lane row, then the partner row (lane ^ 16)
+    // sum over the wavefront: DPP rotations inside each 16-lane row, then the
+    // partner rows (lane ^ 16, lane ^ 32)
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-        float a = acc[t];
-        a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x128, 0xf, 0xf, false));  // row_ror:8
-        a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x124, 0xf, 0xf, false));  // row_ror:4
-        a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x122, 0xf, 0xf, false));  // row_ror:2
-        a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x121, 0xf, 0xf, false));  // row_ror:1
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
-        acc[t] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    if (l32 == 0 && row < N) {
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int t = 0; t < MT; ++t)
-            if (t < M) reinterpret_cast<float *>(reinterpret_cast<char *>(dst) + t * d_nb1)[row] = acc[t];
+        for (int t = 0; t < MT; ++t) {
+            float a = acc[r][t];
+            a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x128, 0xf, 0xf, false));  // row_ror:8
+            a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x124, 0xf, 0xf, false));  // row_ror:4
+            a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x122, 0xf, 0xf, false));  // row_ror:2
+            a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x121, 0xf, 0xf, false));  // row_ror:1
+            const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+            a = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+            const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+            a = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+            if (lane == 0) red[wave][r * MT + t] = a;
+        }
+    __syncthreads();
+    if (tid < R * MT) {
+        const int r = tid / MT, t = tid - r * MT;
+        float o = 0.0f;
+#pragma unroll
+        for (int wv = 0; wv < W; ++wv) o += red[wv][tid];
+        if (t < M && row0 + r < N) reinterpret_cast<float *>(reinterpret_cast<char *>(dst) + t * d_nb1)[row0 + r] = o;
     }
 }
 
@@ -795,7 +772,7 @@ OpLayout op_layout(int64_t K, int64_t M) {
 }  // namespace
 
 size_t out_proj_workspace(int64_t K, int64_t M) {
-    if (M <= kGemvTokens) return 0;  // the decode path keeps its operands in LDS
+    if (M <= kGemvTokens) return 0;  // the decode path keeps its operands in registers
     return op_layout(K, M).total;
 }
 
@@ -804,30 +781,17 @@ int launch_out_proj(const sqa_tensor &w, const sqa_tensor &x, const sqa_tensor *
     const int64_t K = w.ne[0], N = w.ne[1], M = x.ne[1];
     if (M == 0 || N == 0) return SQA_OK;
     if (M <= kGemvTokens) {
-        static std::once_flag lds_once;  // up to 4 x 16K floats of activations
-        static hipError_t lds_err = hipSuccess;
-        std::call_once(lds_once, [] {
-            for (const void *f : {(const void *)op_gemv_kernel<1, true>, (const void *)op_gemv_kernel<2, true>,
-                                  (const void *)op_gemv_kernel<4, true>, (const void *)op_gemv_kernel<1, false>,
-                                  (const void *)op_gemv_kernel<2, false>, (const void *)op_gemv_kernel<4, false>})
-                if (lds_err == hipSuccess)
-                    lds_err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kGemvMaxLds);
-        });
-        if (lds_err != hipSuccess) return hip_status(lds_err, "out_proj LDS attribute");
         const int mt = M == 1 ? 1 : (M == 2 ? 2 : 4);
-        const size_t lds = (size_t)mt * (K / kQK * kGemvSbStride + K / 32) * sizeof(float);
-        if (lds > (size_t)kGemvMaxLds)
-            return set_error(SQA_ERR_UNSUPPORTED, "out_proj: K = %lld too large for %d tokens", (long long)K, (int)M);
         const int prof = profile_start("out_proj", s);
         const uint8_t *wd = (const uint8_t *)w.data;
         const char *xd = (const char *)x.data, *gd = gate ? (const char *)gate->data : nullptr;
         const int64_t wn = (int64_t)w.nb[1], xn = (int64_t)x.nb[1], gn = gate ? (int64_t)gate->nb[1] : 0;
         float *dd = (float *)dst.data;
         const int64_t dn = (int64_t)dst.nb[1];
-        const dim3 grid((unsigned)(N / 8));
+        const dim3 grid((unsigned)(N / kGemvRows));
         const bool vec = (uintptr_t)xd % 16 == 0 && xn % 16 == 0 && (!gd || ((uintptr_t)gd % 16 == 0 && gn % 16 == 0));
 #define SQA_GEMV(MTV)                                                                                          \
-    (vec ? op_gemv_kernel<MTV, true> : op_gemv_kernel<MTV, false>)<<<grid, dim3(256), lds, s>>>(               \
+    (vec ? op_gemv_kernel<MTV, true> : op_gemv_kernel<MTV, false>)<<<grid, dim3(kGemvThreads), 0, s>>>(        \
         wd, wn, xd, xn, gd, gn, (int)K, (int)N, (int)M, dd, dn)
         if (mt == 1)
             SQA_GEMV(1);
