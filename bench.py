@@ -452,6 +452,31 @@ def cpu_prefill_baseline(orc, np, n_pos=16, seed=11):
                       f"{layer_s * 1e3:.0f} ms per layer"}
 
 
+def summarize_trace(trace_dir):
+    """One row per (kernel, grid, workgroup size) of the rocprofv3 kernel traces
+    (*kernel_trace.csv) under trace_dir: launches and the median, mean and
+    minimum duration. Kernels of one name launched at different grids (the
+    decode kernel at different KV lengths) fall in different rows; shapes that
+    share a grid are profiled in separate runs (--main-nkv)."""
+    import csv
+    import glob
+    import statistics
+    groups = {}
+    for f in sorted(glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
+                name = name.replace("void ", "").replace("sqa::", "")
+                grid = r.get("Grid_Size") or r.get("Grid_Size_X", "?")
+                wg = r.get("Workgroup_Size") or r.get("Workgroup_Size_X", "?")
+                key = (name, grid, wg)
+                groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print(f"{'kernel':48s} {'grid':>8s} {'wg':>5s} {'launches':>8s} {'median us':>10s} {'mean us':>9s} {'min us':>8s}")
+    for (name, grid, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        print(f"{name[:48]:48s} {grid:>8s} {wg:>5s} {len(d):8d} {statistics.median(d):10.2f} "
+              f"{statistics.mean(d):9.2f} {min(d):8.2f}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -468,7 +493,14 @@ def main():
     ap.add_argument("--no-out-proj", action="store_true", help="skip the W_o projection leg")
     ap.add_argument("--copy-ref", action="store_true",
                     help="run a plain 256 MiB device copy at the end (counter calibration)")
+    ap.add_argument("--main-nkv", type=int, default=N_KV,
+                    help="KV length of the main decode leg (profiling aid; the headline is 172032)")
+    ap.add_argument("--summarize-trace", metavar="DIR",
+                    help="print per-(kernel, grid) durations of the rocprofv3 kernel traces under DIR and exit")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of this single-GPU path; --gpus {args.gpus} is not "
               "supported: the path runs on one GPU and has no multi-GPU mode", file=sys.stderr)
@@ -484,20 +516,21 @@ def main():
     torch.manual_seed(0)
 
     ks, vs = fill_caches(sqa, torch, dev, N_LAYERS, N_KV, seed=1)
+    n_main = min(args.main_nkv, N_KV)
     qs = [torch.randn((1, H, D), device=dev, dtype=torch.float32) for _ in range(N_LAYERS)]
-    mask = torch.zeros((1, N_KV), dtype=torch.float16, device=dev)  # decode: every key visible
+    mask = torch.zeros((1, n_main), dtype=torch.float16, device=dev)  # decode: every key visible
     out = torch.empty((1, H, D), dtype=torch.float32, device=dev)
-    ws = torch.empty(sqa.flash_attn_workspace_size(qs[0], ks[0], N_KV), dtype=torch.uint8, device=dev)
+    ws = torch.empty(sqa.flash_attn_workspace_size(qs[0], ks[0], n_main), dtype=torch.uint8, device=dev)
 
     def step():
         for li in range(N_LAYERS):
-            sqa.flash_attn_ext(qs[li], ks[li], vs[li], N_KV, mask=mask, out=out, workspace=ws)
+            sqa.flash_attn_ext(qs[li], ks[li], vs[li], n_main, mask=mask, out=out, workspace=ws)
 
     for _ in range(args.warmup):
         step()
     ms = time_steps(torch, step, args.steps)
     ms_per_step = ms / args.steps
-    bytes_step = N_LAYERS * layer_bytes(N_KV, 1)
+    bytes_step = N_LAYERS * layer_bytes(n_main, 1)
     value = bytes_step / (ms_per_step * 1e-3) / 1e9
 
     # Per-kernel durations with HIP events on the launch stream (same steps again).
@@ -510,7 +543,7 @@ def main():
     kernels = {"fa_decode": round(dec_avg_us, 2)}
     if comb_n:
         kernels["fa_combine"] = round(comb_ms / comb_n * 1e3, 2)
-    achieved = layer_bytes(N_KV, 1) / (dec_avg_us * 1e-6) / 1e9
+    achieved = layer_bytes(n_main, 1) / (dec_avg_us * 1e-6) / 1e9
 
     result = {
         "metric": "q4_0 FA decode HBM GB/s @172K ctx (% peak); pp512 attn TFLOP/s (% MFMA)",
@@ -525,16 +558,16 @@ def main():
         "vs_baseline": None,
         "dtype": "q4_0 KV, q8_0 Q: int8 MFMA (QK) + fp16 MFMA (PV), fp32 accumulate",
         "data": "synthetic (seeded N(0,1) Q/K/V; K/V quantized on the GPU)",
-        "config": {"workload": "decode n_q=1, 16q/2kv heads, hd256, q4_0 K/V, n_kv=172032, "
-                               "10 independent layers, F16 mask", "n_kv": N_KV, "layers": N_LAYERS,
+        "config": {"workload": f"decode n_q=1, 16q/2kv heads, hd256, q4_0 K/V, n_kv={n_main}, "
+                               "10 independent layers, F16 mask", "n_kv": n_main, "layers": N_LAYERS,
                    "n_q": 1, "heads": H, "kv_heads": HKV, "head_dim": D},
         "per_layer_us": round(ms_per_step * 1e3 / N_LAYERS, 2),
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "kernels_us": kernels,
         "roofline": {"kernel": "fa_decode", "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": DECODE_TRAFFIC_BYTES,
-                     "bytes_per_launch": layer_bytes(N_KV, 1)},
+                     "traffic": DECODE_TRAFFIC_BYTES if n_main == N_KV else None,
+                     "bytes_per_launch": layer_bytes(n_main, 1)},
     }
 
     # The same 10-layer step captured once in a HIP graph and replayed: the
@@ -574,22 +607,22 @@ def main():
     if not args.no_cpu:
         from oracle import oracle as orc
 
-        kq = ks[0].cpu().numpy()
-        vq = vs[0].cpu().numpy()
+        kq = ks[0][:n_main].cpu().numpy()
+        vq = vs[0][:n_main].cpu().numpy()
         qh = qs[0].cpu().numpy()
         mh = mask.cpu().numpy()
         dt, threads, reps = cpu_baseline(orc, kq, vq, qh, mh)
         model, ncpu = host_cpu()
-        result["cpu_baseline"] = {"value": round(layer_bytes(N_KV, 1) / dt / 1e9, 3), "unit": "GB/s",
+        result["cpu_baseline"] = {"value": round(layer_bytes(n_main, 1) / dt / 1e9, 3), "unit": "GB/s",
                                   "cores": threads, "kind": "port",
-                                  "sample": f"{reps} runs of one 172032-key decode layer (n_q=1, 16 rows); "
+                                  "sample": f"{reps} runs of one {n_main}-key decode layer (n_q=1, 16 rows); "
                                             f"{dt * 1e3:.1f} ms per layer",
                                   "host_cpu": model, "host_logical_cpus": ncpu,
                                   "build": "gcc -O3 -march=x86-64-v3 -fopenmp, one (query, head) row per thread"}
         if not args.no_prefill:
             result["cpu_baseline_prefill_pp512"] = cpu_prefill_baseline(orc, np)
         # Check the timed GPU output of that layer against the oracle.
-        o_gpu = sqa.flash_attn_ext(qs[0], ks[0], vs[0], N_KV, mask=mask).cpu().numpy()
+        o_gpu = sqa.flash_attn_ext(qs[0], ks[0], vs[0], n_main, mask=mask).cpu().numpy()
         o_ref = orc.flash_attn_ext(qh, kq, vq, mh, threads=threads)
         rms = float(np.sqrt(np.mean(o_ref.astype(np.float64) ** 2)))
         result["parity_max_err_over_rms"] = float(np.abs(o_gpu - o_ref).max() / rms)
