@@ -99,19 +99,21 @@ def capture(torch, fn):
     return g
 
 
-def verify_leg(sqa, torch, dev, ks, vs, steps):
+def verify_leg(sqa, torch, dev, ks, vs, steps, lengths=(32768, 131072, N_KV), graphs=True):
     """MTP verify (n_q = 2: the current token plus one draft, causal across the
     two rows) against plain decode (n_q = 1) over the first n_kv rows of the 10
-    layers' caches, at 32768, 131072 and 172032 keys. Each 10-layer step is
+    layers' caches, at each KV length in lengths (32768, 131072 and 172032
+    keys by default). Each 10-layer step is
     captured in a HIP graph and replayed, so the figures are GPU time (at 32K a
     layer takes less GPU time than the Python wrapper takes to launch it, and
     eager launches would time the host); the two step kinds alternate within
     one loop, each bracketed by its own events, so the marginal cost of the
     draft row is a difference of neighbouring steps. Kernel times come from one
     more eager pass with the library's event hooks; roofline = algorithmic
-    bytes / fa_decode time."""
+    bytes / fa_decode time. graphs=False times eager launches instead (for
+    counter collection, which serialises every dispatch)."""
     out = {}
-    for n_kv in (32768, 131072, N_KV):
+    for n_kv in lengths:
         q1 = torch.randn((1, H, D), device=dev)
         q2 = torch.randn((2, H, D), device=dev)
         m1 = torch.empty((1, n_kv), dtype=torch.float16, device=dev)
@@ -129,18 +131,23 @@ def verify_leg(sqa, torch, dev, ks, vs, steps):
 
         run1 = lambda: run(q1, m1, o1, w1)
         run2 = lambda: run(q2, m2, o2, w2)
-        g1, g2 = capture(torch, run1), capture(torch, run2)
+        if graphs:
+            g1, g2 = capture(torch, run1), capture(torch, run2)
+            rep1, rep2 = g1.replay, g2.replay
+        else:
+            g1 = g2 = None
+            rep1, rep2 = run1, run2
         for _ in range(3):
-            g1.replay()
-            g2.replay()
+            rep1()
+            rep2()
         rounds = max(10, steps)
         ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(rounds)]
         torch.cuda.synchronize()
         for r in range(rounds):
             ev[r][0].record()
-            g1.replay()
+            rep1()
             ev[r][1].record()
-            g2.replay()
+            rep2()
             ev[r][2].record()
         torch.cuda.synchronize()
         t1 = sorted(e[0].elapsed_time(e[1]) for e in ev)
@@ -168,9 +175,10 @@ def verify_leg(sqa, torch, dev, ks, vs, steps):
             "marginal_pct_iqr": [round(100 * marg[len(marg) // 4], 1), round(100 * marg[3 * len(marg) // 4], 1)],
             "kernels_us": kern,
             "fa_decode_roofline_frac": frac,
-            "timing": "HIP graph replay of the 10-layer step (GPU time); kernels from events, eager",
+            "timing": ("HIP graph replay of the 10-layer step (GPU time)" if graphs else "eager launches")
+                      + "; kernels from events, eager",
             "rounds": rounds}
-        del g1, g2
+        del g1, g2, rep1, rep2
     return out
 
 
@@ -333,7 +341,7 @@ def producer_leg(sqa, torch, dev, steps, warmup):
     return out
 
 
-def out_proj_leg(sqa, torch, dev, np, steps, warmup):
+def out_proj_leg(sqa, torch, dev, np, steps, warmup, graphs=True):
     """W_o projection per layer (attn.rs:281-285): dst = W . (x * sigmoid(gate)) with
     W a Q4_K [4096, 2048] weight (n_head 16 x head_dim 256 in, n_embd 2048 out) of
     random codes and scales, for a decode token, a 2-token verify and the 512-token
@@ -367,17 +375,18 @@ def out_proj_leg(sqa, torch, dev, np, steps, warmup):
         sqa.profile_end()
         tt, c = sqa.profile_get("out_proj")
         us = tt / c * 1e3
-        g = capture(torch, step)  # the same 10 layers without the Python launch cost
-        for _ in range(2):
-            g.replay()
-        ms_g = time_steps(torch, g.replay, steps) / steps
-        del g
-        gl = ms_g * 1e3 / N_LAYERS
         out[f"m{M}"] = {"per_layer_us": round(ms * 1e3 / N_LAYERS, 2), "kernels_us": round(us, 2),
-                        "graph_per_layer_us": round(gl, 2),
                         "weight_GB/s": round(w_bytes / (us * 1e-6) / 1e9, 1),
-                        "graph_weight_GB/s": round(w_bytes / (gl * 1e-6) / 1e9, 1),
                         "TFLOP/s": round(2 * N * K * M / (us * 1e-6) / 1e12, 2)}
+        if graphs:
+            g = capture(torch, step)  # the same 10 layers without the Python launch cost
+            for _ in range(2):
+                g.replay()
+            ms_g = time_steps(torch, g.replay, steps) / steps
+            del g
+            gl = ms_g * 1e3 / N_LAYERS
+            out[f"m{M}"]["graph_per_layer_us"] = round(gl, 2)
+            out[f"m{M}"]["graph_weight_GB/s"] = round(w_bytes / (gl * 1e-6) / 1e9, 1)
     out["shape"] = {"K": K, "N": N, "weight": "Q4_K", "weight_bytes": w_bytes}
     return out
 
@@ -452,12 +461,25 @@ def cpu_prefill_baseline(orc, np, n_pos=16, seed=11):
                       f"{layer_s * 1e3:.0f} ms per layer"}
 
 
+def _trace_key(r):
+    name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
+    name = name.replace("void ", "").replace("sqa::", "")
+    def total(prefix):  # work-items over all dimensions (traces list X, Y and Z apart)
+        if r.get(prefix):
+            return r[prefix]
+        dims = [r.get(f"{prefix}_{a}") for a in "XYZ"]
+        return str(int(dims[0]) * int(dims[1] or 1) * int(dims[2] or 1)) if dims[0] else "?"
+    return name, total("Grid_Size"), total("Workgroup_Size")
+
+
 def summarize_trace(trace_dir):
     """One row per (kernel, grid, workgroup size) of the rocprofv3 kernel traces
     (*kernel_trace.csv) under trace_dir: launches and the median, mean and
     minimum duration. Kernels of one name launched at different grids (the
     decode kernel at different KV lengths) fall in different rows; shapes that
-    share a grid are profiled in separate runs (--main-nkv)."""
+    share a grid are profiled in separate runs (--main-nkv, --verify-nkv).
+    Counter collections (*counter_collection.csv) under trace_dir give one row
+    per (kernel, grid, workgroup size, counter): the mean value per dispatch."""
     import csv
     import glob
     import statistics
@@ -465,16 +487,27 @@ def summarize_trace(trace_dir):
     for f in sorted(glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)):
         with open(f) as fh:
             for r in csv.DictReader(fh):
-                name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
-                name = name.replace("void ", "").replace("sqa::", "")
-                grid = r.get("Grid_Size") or r.get("Grid_Size_X", "?")
-                wg = r.get("Workgroup_Size") or r.get("Workgroup_Size_X", "?")
-                key = (name, grid, wg)
-                groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    print(f"{'kernel':48s} {'grid':>8s} {'wg':>5s} {'launches':>8s} {'median us':>10s} {'mean us':>9s} {'min us':>8s}")
+                d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+                groups.setdefault(_trace_key(r), []).append(d)
+    if groups:
+        print(f"{'kernel':48s} {'grid':>8s} {'wg':>5s} {'launches':>8s} {'median us':>10s} {'mean us':>9s} "
+              f"{'min us':>8s}")
     for (name, grid, wg), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
         print(f"{name[:48]:48s} {grid:>8s} {wg:>5s} {len(d):8d} {statistics.median(d):10.2f} "
               f"{statistics.mean(d):9.2f} {min(d):8.2f}")
+    per_dispatch = {}
+    for f in sorted(glob.glob(os.path.join(trace_dir, "**", "*counter_collection.csv"), recursive=True)):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                key = _trace_key(r) + (r["Counter_Name"],)
+                disp = (f, r.get("Dispatch_Id") or r.get("Correlation_Id"))
+                slot = per_dispatch.setdefault(key, {})
+                slot[disp] = slot.get(disp, 0.0) + float(r["Counter_Value"])
+    if per_dispatch:
+        print(f"{'kernel':48s} {'grid':>8s} {'wg':>5s} {'counter':24s} {'dispatches':>10s} {'mean per dispatch':>18s}")
+    for (name, grid, wg, counter), v in sorted(per_dispatch.items()):
+        print(f"{name[:48]:48s} {grid:>8s} {wg:>5s} {counter:24s} {len(v):10d} "
+              f"{statistics.mean(v.values()):18.1f}")
 
 
 def main():
@@ -489,14 +522,18 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the pp512 prefill leg")
     ap.add_argument("--no-stack", action="store_true", help="skip the 10-layer ubatch-2048 stack leg")
     ap.add_argument("--no-producer", action="store_true", help="skip the K/Q producer (norm + rope) leg")
-    ap.add_argument("--no-graph", action="store_true", help="skip the graph-replay decode timing")
+    ap.add_argument("--no-graph", action="store_true", help="no HIP graphs: skip the graph-replay decode timing; the verify and W_o legs "
+                         "time eager launches (for counter collection)")
     ap.add_argument("--no-out-proj", action="store_true", help="skip the W_o projection leg")
     ap.add_argument("--copy-ref", action="store_true",
                     help="run a plain 256 MiB device copy at the end (counter calibration)")
     ap.add_argument("--main-nkv", type=int, default=N_KV,
                     help="KV length of the main decode leg (profiling aid; the headline is 172032)")
+    ap.add_argument("--verify-nkv", type=int, nargs="+", default=[32768, 131072, N_KV],
+                    help="KV lengths of the verify leg (profiling aid: one length per run gives one trace row each)")
     ap.add_argument("--summarize-trace", metavar="DIR",
-                    help="print per-(kernel, grid) durations of the rocprofv3 kernel traces under DIR and exit")
+                    help="print per-(kernel, grid) durations (kernel traces) and counter means (counter "
+                         "collections) of the rocprofv3 output under DIR and exit")
     args = ap.parse_args()
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
@@ -589,7 +626,9 @@ def main():
         del graph
 
     if not args.no_verify:
-        result["verify_nq2"] = verify_leg(sqa, torch, dev, ks, vs, args.steps)
+        result["verify_nq2"] = verify_leg(sqa, torch, dev, ks, vs, args.steps,
+                                             tuple(min(n, N_KV) for n in args.verify_nkv),
+                                             graphs=not args.no_graph)
 
     if not args.no_prefill:
         result["prefill_pp512"] = prefill_leg(sqa, torch, dev, max(2, args.steps // 2), 2)
@@ -601,7 +640,8 @@ def main():
         result["producer_rope_norm"] = producer_leg(sqa, torch, dev, max(2, args.steps // 2), 2)
         torch.cuda.empty_cache()
     if not args.no_out_proj:
-        result["out_proj_wo"] = out_proj_leg(sqa, torch, dev, np, max(2, args.steps // 2), 2)
+        result["out_proj_wo"] = out_proj_leg(sqa, torch, dev, np, max(2, args.steps // 2), 2,
+                                             graphs=not args.no_graph)
         torch.cuda.empty_cache()
 
     if not args.no_cpu:
