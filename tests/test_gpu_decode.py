@@ -46,6 +46,22 @@ def test_decode_ragged_lengths(sqa, orc, dev, n_kv, start):
     assert rel_err(got, ref) <= TOL
 
 
+@pytest.mark.parametrize("n_q", [1, 2])
+@pytest.mark.parametrize("n_kv", [1000, 4096, 8192, 12345, 16384, 24001, 40000])
+def test_short_contexts_across_split_regimes(sqa, orc, dev, n_q, n_kv):
+    """The split count fills one workgroup per CU while tiles last, so short
+    contexts run one-tile splits (up to 8K keys on 256 CUs), then 2-4 tiles per
+    split, and from ~32K the four-tile rule; ragged lengths end mid-tile. The
+    causal rows of an MTP verify and outlier channels at every length."""
+    q, kq, vq = qkv(orc, 3000 + n_kv + n_q, n_q, n_kv, outliers=5)
+    mask = orc.causal_mask(n_q, n_kv, n_kv - n_q)
+    ref = orc.flash_attn_ext(q, kq, vq, mask)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    err = rel_err(got, ref)
+    print(f"n_q={n_q} n_kv={n_kv}: max err / rms = {err:.3e}")
+    assert err <= TOL
+
+
 @pytest.mark.parametrize("n_kv", [512, 32768])
 def test_verify_two_rows_causal(sqa, orc, dev, n_kv):
     """MTP verify: n_q=2, row 0 sees n_kv-1 keys, row 1 sees n_kv (graph.rs:554-560)."""
