@@ -49,7 +49,11 @@
 //     no rescale. A score wavefront that sees such a logit uses the larger max
 //     for its own P and raises a flag; on the next tile every wavefront of the
 //     workgroup reads the four maxima used, takes their maximum, and rescales
-//     its share (l, O, and the P values of that tile) onto it.
+//     its share (l, O, and the P values of that tile) onto it. In the form of
+//     up to 8 rows, the four score wavefronts exchange their row maxima on a
+//     split's first tile (one more barrier), so that tile starts from the
+//     common maximum and nothing is rescaled; the 16-row form has no registers
+//     to spare for it (two workgroups per CU need <= 128 VGPRs).
 //   * PV: v_mfma_f32_16x16x32_f16 with fp32 accumulation, d_v on the A side:
 //     A = P d_v 2^E of the block as an exact fp16 hi + lo pair (P arrives as an
 //     fp16 hi + lo pair, ~22 bits), B = the raw nibbles as fp16 subnormals (nib
@@ -543,12 +547,25 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             }
             // -- softmax weights under the reference max (lazy, see the header) ---
             const float lim = m_ref + kSlack;
-            const bool need = __any((s[0] > lim) | (s[1] > lim) | (s[2] > lim) | (s[3] > lim));
+            bool need = __any((s[0] > lim) | (s[1] > lim) | (s[2] > lim) | (s[3] > lim));
             float mu = m_ref;
             if (need) {
                 float mt = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
                 mt = xmax32(xmax16(mt));
                 mu = fmaxf(m_ref, mt);
+            }
+            if (!TWO && t == 0) {
+                // The split's first tile (m_ref = -inf, so mu is this wavefront's
+                // row maximum), up to 8 rows: the four score wavefronts agree on
+                // each row's maximum over all 64 keys (through lbuf, free until the
+                // statistics, and one more barrier, which the value wavefronts
+                // match) and start from it, so the tile's P needs no rescale by the
+                // value wavefronts and no maximum has moved.
+                if (g == 0 && row_writer) lbuf[wq * 16 + my_r] = mu;
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // first-tile maxima
+                mu = fmaxf(fmaxf(lbuf[my_r], lbuf[16 + my_r]), fmaxf(lbuf[32 + my_r], lbuf[48 + my_r]));
+                m_ref = mu;
+                need = false;
             }
             m_used = mu;
             // the reference plus the P shift: exact while |mu| < 2^21
@@ -785,7 +802,11 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             kn += tile_bytes;
             vn += tile_bytes;
             c = c1;
-            if (t == 0) continue;
+            if (t == 0) {
+                // the score wavefronts' first-tile maxima exchange (no tile, no barrier)
+                if (!TWO && n_tiles > 0) asm volatile("s_barrier" ::: "memory");
+                continue;
+            }
 
             const int tv = t - 1;  // PV of the tile whose P the score wavefronts wrote last
             const int pb = tv & 1;
@@ -853,6 +874,12 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                 }
             }
 
+            // -- the split's first tile: P is relative to the rows' common maxima
+            if (!TWO && tv == 0) {
+                const float *mr = mbuf + pb * 64;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) m_acc[i] = mr[(4 * g + i) & kRowMask];
+            }
             // -- a possible move of the reference max ---------------------------------
             if ((fl.x | fl.y | fl.z | fl.w) & 1u) {
                 const float *mr = mbuf + pb * 64;
