@@ -618,9 +618,23 @@ __global__ __launch_bounds__(64 * kG2Waves) void op_gemm2_kernel(Gemm2Params p) 
 // of an fp16 is code * 2^-24, a high nibble left in bits 4-7 is code * 2^-20,
 // and the 2^24 or 2^20 goes into the scale. The gate's sigmoid is 1/(1 + 2^(-g
 // log2 e)) from the hardware exp2 and reciprocal (about 2 ulp). The partial
-// sums of each (row, token) are added by DPP row rotations and lane swaps
-// inside each wavefront, then across the wavefronts through LDS. VEC: x (and
-// gate) rows are 16-byte aligned and read four floats at a time.
+// sums of the (row, token) pairs are added by recursive halving inside each
+// wavefront (lane swaps and DPP moves, each lane ending with one pair's sum),
+// then across the wavefronts through LDS. VEC: x (and gate) rows are 16-byte
+// aligned and read four floats at a time.
+// One halving step of the GEMV's wavefront sum (below): values a[0 .. 2N) to
+// a[0 .. N), the lane with `up` clear keeping the lower half, plus the
+// partner's copy of the kept half moved by the DPP control CTRL.
+template <int N, int CTRL>
+__device__ __forceinline__ void halve_dpp(float *a, bool up) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        const float keep = up ? a[N + j] : a[j];
+        const float give = up ? a[j] : a[N + j];
+        a[j] = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(give), CTRL, 0xf, 0xf, false));
+    }
+}
+
 constexpr int kGemvRows = 8;
 constexpr int kGemvThreads = 512;
 template <int MT, bool VEC>
@@ -723,23 +737,43 @@ __global__ __launch_bounds__(kGemvThreads) void op_gemv_kernel(const uint8_t *__
         }
     }
 #undef SQA_MIX
-    // sum over the wavefront: DPP rotations inside each 16-lane row, then the
-    // partner rows (lane ^ 16, lane ^ 32)
+    // Sum of the V = R * MT values (index r * MT + t) over the wavefront by
+    // recursive halving: each step pairs lanes that differ in one bit; the lane
+    // with the bit clear keeps the lower half of its values, the other the
+    // upper half, each adding its partner's copy of the half it keeps. Lane bits
+    // 5 and 4 swap halves between rows (permlane32 / permlane16 swaps, which
+    // exchange the upper 32 lanes of the first operand with the lower 32 of the
+    // second and the odd rows of the first with the even rows of the second: a
+    // swap and an add per pair), bit 3 pairs lane ^ 8 (row_ror:8), bit 2 lane ^ 7
+    // (row_half_mirror: the same bits above 2), bit 1 lane ^ 2 (quad_perm), and
+    // the bits left over are summed in place. Lane l then holds the full sum of
+    // index l >> (6 - log2 V): V - 1 swaps or DPP moves instead of 6 V.
+    constexpr int V = R * MT;
+    static_assert(V == 8 || V == 16 || V == 32, "halving steps below");
+    float a[V];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            float a = acc[r][t];
-            a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x128, 0xf, 0xf, false));  // row_ror:8
-            a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x124, 0xf, 0xf, false));  // row_ror:4
-            a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x122, 0xf, 0xf, false));  // row_ror:2
-            a += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x121, 0xf, 0xf, false));  // row_ror:1
-            const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(a), false, false);
-            a = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
-            const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
-            a = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
-            if (lane == 0) red[wave][r * MT + t] = a;
-        }
+        for (int t = 0; t < MT; ++t) a[r * MT + t] = acc[r][t];
+#pragma unroll
+    for (int j = 0; j < V / 2; ++j) {  // bit 5
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[j]), __float_as_uint(a[V / 2 + j]), false, false);
+        a[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+#pragma unroll
+    for (int j = 0; j < V / 4; ++j) {  // bit 4
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[j]), __float_as_uint(a[V / 4 + j]), false, false);
+        a[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    halve_dpp<V / 8, 0x128>(a, (lane & 8) != 0);                   // bit 3, lane ^ 8 (row_ror:8)
+    if constexpr (V >= 16) halve_dpp<V / 16, 0x141>(a, (lane & 4) != 0);  // bit 2, lane ^ 7 (row_half_mirror)
+    if constexpr (V >= 32) halve_dpp<V / 32, 0x4e>(a, (lane & 2) != 0);   // bit 1, lane ^ 2 (quad_perm [2,3,0,1])
+    float s = a[0];
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0xb1, 0xf, 0xf, false));  // lane ^ 1
+    if constexpr (V <= 16) s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x4e, 0xf, 0xf, false));
+    if constexpr (V <= 8) s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x141, 0xf, 0xf, false));
+    constexpr int kSpan = 64 / V;  // lanes that share an index
+    if ((lane & (kSpan - 1)) == 0) red[wave][lane / kSpan] = s;
     __syncthreads();
     if (tid < R * MT) {
         const int r = tid / MT, t = tid - r * MT;
