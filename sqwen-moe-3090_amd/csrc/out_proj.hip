@@ -607,9 +607,11 @@ __global__ __launch_bounds__(64 * kG2Waves) void op_gemm2_kernel(Gemm2Params p) 
 // kGemvThreads threads takes kGemvRows rows of W. Thread t owns the 8
 // activations k = 8t .. 8t + 7 (and the same slice of every further
 // 8 * kGemvThreads values of K) for all of those rows, so it loads its slice of
-// x and gate once and, for each row, the slice's 8 code bytes and the
-// super-block header, all before it uses any of them: one memory latency, then
-// arithmetic, then one reduction.
+// x and gate once and, for each row, the slice's 8 code bytes, all before it
+// uses any of them: one memory latency, then arithmetic, then one reduction.
+// The four threads of a lane quad share one 32-value sub-block: each loads and
+// unpacks the super-block headers of two of the 8 rows, and the quad
+// broadcasts the rows' scales.
 //   Value 64j + 16h2 + i of a super-block sits in byte 32j + 16(h2 & 1) + i of
 //   its codes, low nibble for h2 < 2, high for h2 >= 2; sub-block 2j + (h2 >> 1).
 // Per row and token: out += d * scale * sum(code * xg) - dmin * min * sum(xg).
@@ -622,6 +624,12 @@ __global__ __launch_bounds__(64 * kG2Waves) void op_gemm2_kernel(Gemm2Params p) 
 // wavefront (lane swaps and DPP moves, each lane ending with one pair's sum),
 // then across the wavefronts through LDS. VEC: x (and gate) rows are 16-byte
 // aligned and read four floats at a time.
+// Lane K of each quad's x in all four lanes of the quad (quad_perm [K,K,K,K]).
+template <int K>
+__device__ __forceinline__ float quad_bcast(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), K * 0x55, 0xf, 0xf, false));
+}
+
 // One halving step of the GEMV's wavefront sum (below): values a[0 .. 2N) to
 // a[0 .. N), the lane with `up` clear keeping the lower half, plus the
 // partner's copy of the kept half moved by the DPP control CTRL.
@@ -661,15 +669,18 @@ __global__ __launch_bounds__(kGemvThreads) void op_gemv_kernel(const uint8_t *__
         const float cscale = hi_nib ? 1048576.0f : 16777216.0f;     // 2^20 or 2^24
         const int s = 2 * j + (h2 >> 1);                            // sub-block
         const int cb = 16 + 32 * j + 16 * (h2 & 1) + (v & 8);       // the slice's first code byte
-        // weights of all rows first (header, 8 code bytes), then the activations
-        uint4 hdr[R];
+        // weights first (8 code bytes of every row; the super-block headers of
+        // rows 2 qd and 2 qd + 1 only, see below), then the activations
+        const int qd = lane & 3;  // the lane quad shares one sub-block (32 values)
+        uint4 hdr[2];
         uint2 q[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint8_t *blk = w + (int64_t)(row0 + r) * w_nb1 + (int64_t)sb * kBlockBytes;
-            hdr[r] = *reinterpret_cast<const uint4 *>(blk);
-            q[r] = *reinterpret_cast<const uint2 *>(blk + cb);
-        }
+        for (int u = 0; u < 2; ++u)
+            hdr[u] = *reinterpret_cast<const uint4 *>(w + (int64_t)(row0 + 2 * qd + u) * w_nb1 +
+                                                      (int64_t)sb * kBlockBytes);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            q[r] = *reinterpret_cast<const uint2 *>(w + (int64_t)(row0 + r) * w_nb1 + (int64_t)sb * kBlockBytes + cb);
         float xg[MT][8];
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
@@ -701,6 +712,31 @@ __global__ __launch_bounds__(kGemvThreads) void op_gemv_kernel(const uint8_t *__
                 xg[t][i] = ok ? xg[t][i] : 0.0f;
             }
         }
+        // d * scale * 2^24 (or 2^20) and dmin * min of sub-block s for the 8 rows:
+        // the four lanes of a quad share s, so lane qd unpacks rows 2 qd and
+        // 2 qd + 1 (ggml's get_scale_min_k4, branch-free) and the quad
+        // broadcasts them (quad_perm [k,k,k,k])
+        float dsu[2], dmu[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t q0 = hdr[u].y, q1 = hdr[u].z, q2 = hdr[u].w;
+            const uint32_t lo_sh = 8u * (uint32_t)(s & 3);
+            const uint32_t sc_lo = (q0 >> lo_sh) & 63u, mn_lo = (q1 >> lo_sh) & 63u;
+            const uint32_t sc_hi = ((q2 >> lo_sh) & 15u) | (((q0 >> (lo_sh + 6u)) & 3u) << 4);
+            const uint32_t mn_hi = ((q2 >> (lo_sh + 4u)) & 15u) | (((q1 >> (lo_sh + 6u)) & 3u) << 4);
+            const uint32_t sc = s < 4 ? sc_lo : sc_hi, mn = s < 4 ? mn_lo : mn_hi;
+            dsu[u] = h2f(hdr[u].x & 0xffffu) * (float)sc * cscale;
+            dmu[u] = h2f(hdr[u].x >> 16) * (float)mn;
+        }
+        float ds[R], dm[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int k = r >> 1;
+            ds[r] = k == 0 ? quad_bcast<0>(dsu[r & 1]) : k == 1 ? quad_bcast<1>(dsu[r & 1])
+                  : k == 2 ? quad_bcast<2>(dsu[r & 1]) : quad_bcast<3>(dsu[r & 1]);
+            dm[r] = k == 0 ? quad_bcast<0>(dmu[r & 1]) : k == 1 ? quad_bcast<1>(dmu[r & 1])
+                  : k == 2 ? quad_bcast<2>(dmu[r & 1]) : quad_bcast<3>(dmu[r & 1]);
+        }
         float sx[MT];  // sum of this slice's activations (the min term)
 #pragma unroll
         for (int t = 0; t < MT; ++t)
@@ -723,17 +759,8 @@ __global__ __launch_bounds__(kGemvThreads) void op_gemv_kernel(const uint8_t *__
                     SQA_MIX(dot[t], xg[t][4 * m + 3], c13, 1);
                 }
             }
-            // 6-bit scale and min of sub-block s (ggml's get_scale_min_k4), branch-free
-            const uint32_t q0 = hdr[r].y, q1 = hdr[r].z, q2 = hdr[r].w;
-            const uint32_t lo_sh = 8u * (uint32_t)(s & 3);
-            const uint32_t sc_lo = (q0 >> lo_sh) & 63u, mn_lo = (q1 >> lo_sh) & 63u;
-            const uint32_t sc_hi = ((q2 >> lo_sh) & 15u) | (((q0 >> (lo_sh + 6u)) & 3u) << 4);
-            const uint32_t mn_hi = ((q2 >> (lo_sh + 4u)) & 15u) | (((q1 >> (lo_sh + 6u)) & 3u) << 4);
-            const uint32_t sc = s < 4 ? sc_lo : sc_hi, mn = s < 4 ? mn_lo : mn_hi;
-            const float ds = h2f(hdr[r].x & 0xffffu) * (float)sc * cscale;
-            const float dm = h2f(hdr[r].x >> 16) * (float)mn;
 #pragma unroll
-            for (int t = 0; t < MT; ++t) acc[r][t] = fmaf(-dm, sx[t], fmaf(ds, dot[t], acc[r][t]));
+            for (int t = 0; t < MT; ++t) acc[r][t] = fmaf(-dm[r], sx[t], fmaf(ds[r], dot[t], acc[r][t]));
         }
     }
 #undef SQA_MIX
