@@ -1,7 +1,9 @@
 // fa_combine.hip - merges the split-KV partials of the decode and prefill
 // attention kernels: out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), with
 // M = max_s m_s (the log-sum-exp rule), optionally times sigmoid(gate) (the
-// output gate of src/model/attn.rs:282-283 in the reference). Partials:
+// output gate of src/model/attn.rs:282-283 in the reference). The weights
+// e^(m_s - M) <= 1 come from the hardware exp2 (about 1 ulp; a weight below
+// 2^-126, negligible beside the largest one of 1, may read as 0). Partials:
 // acc [n_splits][rows][256] unnormalised, ml [n_splits][rows][2] = (m, l) with m
 // in natural-log units of the scaled logits.
 #include "common.hpp"
@@ -10,6 +12,18 @@ namespace sqa {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
+
+// x of lane ^ 16 and of lane ^ 32 through gfx950's row swaps (VALU, no LDS
+// round trip): a swap of x with itself leaves x in one result and the
+// partner's x in the other
+__device__ __forceinline__ float lane_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
 
 // Merge of up to kMaxSplits (256) split partials with one memory latency on the
 // path. Grid: (rows, 16 chunks of 16 dims); 256 threads = 16 dims x 16 split
@@ -44,22 +58,22 @@ __global__ __launch_bounds__(256) void fa_combine_kernel(const float *__restrict
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 16; ++j) m = fmaxf(m, ml[j].x);
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32));
+    m = fmaxf(m, lane_xor16(m));
+    m = fmaxf(m, lane_xor32(m));
     if ((tid & 63) == 0) xm[wv] = m;
     __syncthreads();
     const float M = fmaxf(fmaxf(xm[0], xm[1]), fmaxf(xm[2], xm[3]));
     float o = 0.0f, l = 0.0f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-        const float w = (M == -INFINITY || ml[j].x == -INFINITY) ? 0.0f : exp2f((ml[j].x - M) * kLog2e);
+        const float w = (M == -INFINITY || ml[j].x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((ml[j].x - M) * kLog2e);
         o = fmaf(acc[j], w, o);
         l = fmaf(ml[j].y, w, l);
     }
-    o += __shfl_xor(o, 16);
-    o += __shfl_xor(o, 32);
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    o += lane_xor16(o);
+    o += lane_xor32(o);
+    l += lane_xor16(l);
+    l += lane_xor32(l);
     if ((tid & 63) < 16) xo[wv][dl] = o;
     if ((tid & 63) == 0) xl[wv] = l;
     __syncthreads();
@@ -103,7 +117,7 @@ __global__ __launch_bounds__(256) void fa_combine_rows_kernel(const float *__res
 #pragma unroll
     for (int sp = 0; sp < kRowsMaxSplits; ++sp) {
         if (sp >= n_splits) break;
-        const float w = (M == -INFINITY || ms[sp] == -INFINITY) ? 0.0f : exp2f((ms[sp] - M) * kLog2e);
+        const float w = (M == -INFINITY || ms[sp] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f((ms[sp] - M) * kLog2e);
         L = fmaf(part_ml[((int64_t)sp * rows_total + row) * 2 + 1], w, L);
         const float4 a = *reinterpret_cast<const float4 *>(pa + sp * sstride);
         o.x = fmaf(a.x, w, o.x);
