@@ -295,11 +295,15 @@ def stack_leg(sqa, torch, dev, steps, warmup):
     return res
 
 
-def producer_leg(sqa, torch, dev, steps, warmup):
+def producer_leg(sqa, torch, dev, steps, warmup, graphs=True):
     """K/Q producer per layer: RMSNorm + IMROPE + q4_0 quantize-on-write of the new
     K rows (2 KV heads), and RMSNorm + IMROPE of Q (16 heads, F32 out), for a
     512-token and a 2048-token ubatch. n_rot 64, sections (11, 11, 10, 0),
-    freq_base 1e7 (plausible model values; the kernel takes them as parameters)."""
+    freq_base 1e7 (plausible model values; the kernel takes them as parameters).
+    Kernel times from the event hooks around eager launches include the host's
+    launch gap when the host is the slower side (small kernels); with graphs,
+    the K and Q launches of 10 layers are also captured apart and replayed, which
+    times them on the GPU alone."""
     rope = sqa.rope_params(64, (11, 11, 10, 0), 1e7)
     out = {}
     for n_tok, start in ((PP_N_Q, PP_START), (2048, 131072)):
@@ -337,6 +341,25 @@ def producer_leg(sqa, torch, dev, steps, warmup):
             "k_GB/s": round(k_bytes / (kern["rope_norm_set_rows_q4_0"] * 1e-6) / 1e9, 1),
             "q_GB/s": round(q_bytes / (kern["rope_norm_f32"] * 1e-6) / 1e9, 1),
             "bytes": {"k": k_bytes, "q": q_bytes}}
+        if graphs:
+            def kstep():
+                for _ in range(N_LAYERS):
+                    sqa.rope_norm_set_rows_q4_0(cache, k_src, kw, 1e-6, pos, rope, idx)
+
+            def qstep():
+                for _ in range(N_LAYERS):
+                    sqa.rope_norm_f32(q_out, q_src, qw, 1e-6, pos, rope)
+
+            gk, gq = capture(torch, kstep), capture(torch, qstep)
+            for _ in range(2):
+                gk.replay()
+                gq.replay()
+            k_us = time_steps(torch, gk.replay, steps) / steps * 1e3 / N_LAYERS
+            q_us = time_steps(torch, gq.replay, steps) / steps * 1e3 / N_LAYERS
+            del gk, gq
+            out[f"ubatch{n_tok}"]["graph_kernels_us"] = {"rope_norm_set_rows_q4_0": round(k_us, 2),
+                                                         "rope_norm_f32": round(q_us, 2)}
+            out[f"ubatch{n_tok}"]["graph_q_GB/s"] = round(q_bytes / (q_us * 1e-6) / 1e9, 1)
         del k_src, q_src, cache, q_out
     return out
 
@@ -637,7 +660,8 @@ def main():
         result["stack_ub2048_131k"] = stack_leg(sqa, torch, dev, 2, 1)
         torch.cuda.empty_cache()
     if not args.no_producer:
-        result["producer_rope_norm"] = producer_leg(sqa, torch, dev, max(2, args.steps // 2), 2)
+        result["producer_rope_norm"] = producer_leg(sqa, torch, dev, max(2, args.steps // 2), 2,
+                                                    graphs=not args.no_graph)
         torch.cuda.empty_cache()
     if not args.no_out_proj:
         result["out_proj_wo"] = out_proj_leg(sqa, torch, dev, np, max(2, args.steps // 2), 2,
