@@ -368,7 +368,9 @@ def out_proj_leg(sqa, torch, dev, np, steps, warmup, graphs=True):
     """W_o projection per layer (attn.rs:281-285): dst = W . (x * sigmoid(gate)) with
     W a Q4_K [4096, 2048] weight (n_head 16 x head_dim 256 in, n_embd 2048 out) of
     random codes and scales, for a decode token, a 2-token verify and the 512-token
-    ubatch. Decode is bound by the weight bytes; the ubatch by the MFMA work."""
+    ubatch. Decode is bound by the weight bytes; the ubatch by the MFMA work.
+    graph_launch_floor_us: what one launch of a one-element add costs in the
+    same kind of replayed graph, the floor under any kernel's figure here."""
     K, N = H * D, 2048
     rng = np.random.default_rng(7)
     out = {}
@@ -411,6 +413,19 @@ def out_proj_leg(sqa, torch, dev, np, steps, warmup, graphs=True):
             out[f"m{M}"]["graph_per_layer_us"] = round(gl, 2)
             out[f"m{M}"]["graph_weight_GB/s"] = round(w_bytes / (gl * 1e-6) / 1e9, 1)
     out["shape"] = {"K": K, "N": N, "weight": "Q4_K", "weight_bytes": w_bytes}
+    if graphs:
+        # the floor of any launch in a replayed graph: 10 one-element adds
+        one = torch.zeros(1, device=dev)
+
+        def trivial():
+            for _ in range(N_LAYERS):
+                one.add_(1.0)
+
+        g = capture(torch, trivial)
+        for _ in range(2):
+            g.replay()
+        out["graph_launch_floor_us"] = round(time_steps(torch, g.replay, steps) / steps * 1e3 / N_LAYERS, 2)
+        del g
     return out
 
 
