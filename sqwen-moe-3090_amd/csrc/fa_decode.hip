@@ -27,7 +27,8 @@
 // Memory pipeline
 //   Tiles move from HBM to LDS with global_load_lds_dwordx4 (16 bytes per lane,
 //   no registers): the head's 144 bytes of each 288-byte cache row land in a
-//   160-byte LDS row (nine data chunks and a pad chunk). K (and the tile's F16
+//   144-byte LDS row (nine chunks, 36 dwords: one column of 32 rows spans 8
+//   bank positions, a 160-byte row only 4). K (and the tile's F16
 //   mask rows) go into a ring of 3 stages, issued 2 tiles ahead of the QK that
 //   reads them; V into a ring of 3 stages, issued 1 tile ahead of its tile's QK,
 //   i.e. 2 ahead of the PV that reads it. LDS rows rotate their chunks so that
@@ -96,10 +97,10 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kTileKeys = 64;
 constexpr int kKStages = 3;
 constexpr int kVStages = 3;
-constexpr int kSlotsPerRow = 10;                      // 9 data chunks + a pad chunk
-constexpr int kLdsRow = 16 * kSlotsPerRow;            // 160
-constexpr int kTensorBytes = kTileKeys * kLdsRow;     // 10240
-constexpr int kTensorInsts = kTensorBytes / 1024;     // 10 DMA instructions of 64 x 16 B
+constexpr int kSlotsPerRow = 9;                       // the head row's 9 chunks
+constexpr int kLdsRow = 16 * kSlotsPerRow;            // 144
+constexpr int kTensorBytes = kTileKeys * kLdsRow;     // 9216
+constexpr int kTensorInsts = kTensorBytes / 1024;     // 9 DMA instructions of 64 x 16 B
 constexpr int kMaxMaskRows = 4;                       // query positions
 constexpr int kMaskStageBytes = kMaxMaskRows * kTileKeys * 2;
 constexpr int kPRow = 136;                            // fp16 P row: 64 keys hi, 64 keys lo, 8 pad
@@ -248,8 +249,8 @@ __device__ __forceinline__ int k_rot(int row) { return (row >> 3) & 1; }
 __device__ __forceinline__ int v_rot(int row) { return 2 * ((row >> 3) & 3); }
 
 // Per-lane source offset of DMA instruction j of a tile stage: slot s = 64*j +
-// lane lands at LDS byte 16*s, i.e. slot s % 10 of row s / 10, and holds chunk
-// (slot - rot) mod 10 of that row's head half (chunk 9, the pad, repeats chunk 8).
+// lane lands at LDS byte 16*s, i.e. slot s % 9 of row s / 9, and holds chunk
+// (slot - rot) mod 9 of that row's head half.
 template <bool V>
 __device__ __forceinline__ uint32_t slot_offset(int j, int lane, int kvh, uint32_t row_bytes) {
     const int s = 64 * j + lane;
@@ -257,7 +258,7 @@ __device__ __forceinline__ uint32_t slot_offset(int j, int lane, int kvh, uint32
     const int slot = s - row * kSlotsPerRow;
     int c = slot - (V ? v_rot(row) : k_rot(row));
     c = c < 0 ? c + kSlotsPerRow : c;
-    return (uint32_t)row * row_bytes + (uint32_t)(kvh * kHeadRowBytes + (c < 8 ? c : 8) * 16);
+    return (uint32_t)row * row_bytes + (uint32_t)(kvh * kHeadRowBytes + c * 16);
 }
 // LDS byte of head-row byte c (0..143) of row `row` inside a tile stage
 template <bool V>
@@ -624,8 +625,8 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         // ============ value wavefronts: O[rows][64 dims] += P V =================
         // ---------------- DMA plan of this wavefront ---------------------------
         // Value wavefronts issue every DMA (score wavefronts carry no DMA state):
-        // 10 K + 10 V instructions per tile, K j -> value wave j % 4, V j -> value
-        // wave (j + 2) % 4, the mask rows -> value wave 3 (5 or 6 per wavefront).
+        // 9 K + 9 V instructions per tile, K j -> value wave j % 4, V j -> value
+        // wave (j + 2) % 4, the mask rows -> value wave 3 (4 or 5 per wavefront).
         const int vw = wave - kScoreWaves;
         uint32_t koff[3], voff[3];
         int nk = 0, nv = 0;
@@ -641,8 +642,8 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         const bool mask_dma = p.mask && vw == kValueWaves - 1;
         const int mrow_l = lane >> 3;  // mask DMA lane -> query row, 16-byte segment
         const uint32_t moff = (uint32_t)((int64_t)(mrow_l < p.n_q ? mrow_l : 0) * p.mask_nb1 + 16 * (lane & 7));
-        // every wavefront issues 2 or 3 of the 10 K and of the 10 V instructions
-        static_assert(kTensorInsts == 10 && kValueWaves == 4, "2 or 3 instructions per wavefront and tensor");
+        // every wavefront issues 2 or 3 of the 9 K and of the 9 V instructions
+        static_assert(kTensorInsts == 9 && kValueWaves == 4, "2 or 3 instructions per wavefront and tensor");
         const bool k3 = nk == 3, v3 = nv == 3;
 
         // keys past the cache end re-read its last row (they are masked off); mask
@@ -705,14 +706,15 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         // The wait at interval t: K of tile t and V of tile t-1 must have landed.
         // The loop issues K(t+2) and V(t+1) at interval t, after K 0, K 1 and V 0
         // before the loop, so the younger DMAs at interval t are K(t+1) and V(t):
-        // at least 2 + 2 + 1 = 5 instructions while t + 1 < n_tiles (each wavefront
-        // has 5 tensor instructions per tile pair, the mask wavefront one more), at
-        // least 2 (V(t)) when t + 1 == n_tiles, none at the end. Waiting down to
-        // that lower bound is exact for most wavefronts and, for the one with a
-        // sixth, also waits for the oldest of K(t+1), issued an interval earlier.
+        // at least 2 + 2 = 4 instructions while t + 1 < n_tiles (value wavefront 1
+        // has 2 K and 2 V per tile; 0 and 2 have a third of K or of V, 3 the mask
+        // row when there is a mask), at least 2 (V(t)) when t + 1 == n_tiles, none
+        // at the end. Waiting down to that lower bound is exact for the wavefronts
+        // with 4 and, for those with 5, also waits for the oldest of K(t+1), issued
+        // an interval earlier.
         auto wait_interval = [&](int t) {
             if (t + 1 < n_tiles)
-                asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
             else if (t < n_tiles)
                 asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
             else
