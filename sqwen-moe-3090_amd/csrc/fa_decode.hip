@@ -854,11 +854,21 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                     __builtin_memcpy(&w, &wh, 4);
                     *reinterpret_cast<uint32_t *>(dv_comp + cdst) = w;
                 };
-                store_scaled();
                 // a d_v at or above 2^(11 - E) lowers E so that the largest |d_v| of
                 // the tile lands in [2^8, 2^9); O is rescaled by the exact power of
-                // two and the tile's d_v are stored again
+                // two and the tile's d_v are stored again. On the split's first tile
+                // O is still zero: E comes straight from the tile's largest |d_v|.
                 const uint32_t mag = max(da & 0x7FFFu, db & 0x7FFFu);
+                if (!TWO && tv == 0) {
+                    const int mx = wave_max_u16(mag);
+                    if (mx != 0) {
+                        const int ex = mx >> 10;
+                        const int lg = ex ? ex - 15 : (31 - __clz(mx)) - 24;  // floor(log2 max |d_v|)
+                        set_dv_scale(min(8 - lg, kMaxDvExp));
+                    }
+                    store_scaled();
+                } else {
+                store_scaled();
                 if (__any(mag >= dv_thr)) {
                     const int mx = wave_max_u16(mag);
                     const int ex = mx >> 10;
@@ -873,6 +883,7 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                         set_dv_scale(e_new);
                         store_scaled();
                     }
+                }
                 }
             }
 
