@@ -996,26 +996,43 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         // ---------------- this split's partial O (un-normalised) -----------------
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // pairs the statistics barrier
         const float o_scale = __builtin_amdgcn_ldexpf(1.0f, -e_dv);
-        if (!TWO) {  // C row r + 8 (lanes g + 2 = lane ^ 32) holds the lo part of row r
+        auto store_row = [&](int row, int i) {
+            const int tq = row / p.G, hq = kvh * p.G + row % p.G;
+            float *dst = p.part_acc + ((int64_t)split * rows_total + (int64_t)tq * p.H + hq) * 256 + 64 * dq + n;
+#pragma unroll
+            for (int bl = 0; bl < 2; ++bl) {
+                dst[32 * bl] = fmaf(acc[2 * bl][i], 16777216.0f, -8.0f * cor[bl][i]) * o_scale;
+                dst[32 * bl + 16] = fmaf(acc[2 * bl + 1][i], 1048576.0f, -8.0f * cor[bl][i]) * o_scale;
+            }
+        };
+        if (!TWO) {
+            // C row r + 8 (lanes of group g + 2, lane ^ 32) holds the lo part of row
+            // r: one lane swap per pair of C values adds them, lanes 0-31 keeping
+            // i = 0, 1 (rows 4g + i) and lanes 32-63 i = 2, 3 (rows 4(g - 2) + i),
+            // so every lane stores two rows
+            const bool up = lane >= 32;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                auto fold = [&](floatx4 &x) {
+                    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[i]), __float_as_uint(x[i + 2]),
+                                                                    false, false);
+                    x[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+                };
+#pragma unroll
+                for (int T = 0; T < 4; ++T) fold(acc[T]);
+                fold(cor[0]);
+                fold(cor[1]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int row = up ? 4 * (g - 2) + i + 2 : 4 * g + i;
+                if (row < p.rows) store_row(row, i);
+            }
+        } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-#pragma unroll
-                for (int T = 0; T < 4; ++T) acc[T][i] = xsum32(acc[T][i]);
-                cor[0][i] = xsum32(cor[0][i]);
-                cor[1][i] = xsum32(cor[1][i]);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = 4 * g + i;
-            if (row < p.rows && (TWO || g < 2)) {
-                const int tq = row / p.G, hq = kvh * p.G + row % p.G;
-                float *dst = p.part_acc + ((int64_t)split * rows_total + (int64_t)tq * p.H + hq) * 256 + 64 * dq + n;
-#pragma unroll
-                for (int bl = 0; bl < 2; ++bl) {
-                    dst[32 * bl] = fmaf(acc[2 * bl][i], 16777216.0f, -8.0f * cor[bl][i]) * o_scale;
-                    dst[32 * bl + 16] = fmaf(acc[2 * bl + 1][i], 1048576.0f, -8.0f * cor[bl][i]) * o_scale;
-                }
+                const int row = 4 * g + i;
+                if (row < p.rows) store_row(row, i);
             }
         }
     }
