@@ -13,7 +13,8 @@ bytes of one layer are n_kv*576 (K+V) + 2*16*256*4 (Q, O) + n_kv*2 (mask).
 
 Prints ONE JSON line (rank 0). Extra fields: per-layer microseconds, the
 roofline of the dominant kernel (fa_decode), the CPU oracle timed on this
-host, the MTP verify (n_q = 2) marginal cost, and the prefill leg:
+host, the MTP verify (n_q = 2) marginal cost, the decode time split into a
+per-byte and a fixed part over KV lengths at one split count, and the prefill leg:
 pp512 = a 512-token ubatch appended after 16384 cached tokens (n_kv = 16896,
 causal F16 mask), 10 layers, reported as attention TFLOP/s against the fp16
 MFMA peak. Its FLOPs count QK^T and PV over the keys each query may see:
@@ -180,6 +181,67 @@ def verify_leg(sqa, torch, dev, ks, vs, steps, lengths=(32768, 131072, N_KV), gr
             "rounds": rounds}
         del g1, g2, rep1, rep2
     return out
+
+
+def length_curve_leg(sqa, torch, dev, ks, vs, rounds, lengths=(65536, 98304, 131072, N_KV)):
+    """Decode (n_q = 1, every key visible, as the main leg) at several KV lengths
+    that all run the same split count (256 splits x 2 KV heads on 256 CUs: the
+    split rule reaches its cap from 65536 keys on), so the splits differ only in
+    their number of 64-key tiles. Each 10-layer step is captured in a HIP graph
+    and replayed. A least-squares line through (bytes per layer, time) splits the
+    time into a per-byte part (marginal = the rate at which a longer context
+    streams) and a fixed part (the value at zero bytes: the launches, the first
+    loads' latency, the pipeline fill and drain, the partial stores and the split
+    merge), for the whole layer (graph replay) and for the decode kernel alone
+    (events on eager launches)."""
+    pts = []
+    for n_kv in lengths:
+        q = torch.randn((1, H, D), device=dev)
+        m = torch.zeros((1, n_kv), dtype=torch.float16, device=dev)
+        o = torch.empty((1, H, D), device=dev)
+        wsz = sqa.flash_attn_workspace_size(q, ks[0], n_kv)
+        w = torch.empty(wsz, dtype=torch.uint8, device=dev)
+
+        def run(q=q, m=m, o=o, w=w, n_kv=n_kv):
+            for li in range(N_LAYERS):
+                sqa.flash_attn_ext(q, ks[li], vs[li], n_kv, mask=m, out=o, workspace=w)
+
+        g = capture(torch, run)
+        for _ in range(3):
+            g.replay()
+        t = sorted(time_steps(torch, g.replay, 1) for _ in range(rounds))
+        layer_us = t[len(t) // 2] * 1e3 / N_LAYERS
+        sqa.profile_begin(3 * N_LAYERS * 4 + 16)
+        for _ in range(3):
+            run()
+        torch.cuda.synchronize()
+        sqa.profile_end()
+        dt, dc = sqa.profile_get("fa_decode")
+        # workspace = partials (splits x 16 rows x (1 KiB + 8 B)) + room for a packed mask copy + 256
+        splits = (wsz - 256 - (2 * ((n_kv + 7) // 8 * 8) + 255) // 256 * 256) // (H * D * 4 + H * 2 * 4)
+        pts.append((n_kv, layer_bytes(n_kv, 1), layer_us, dt / dc * 1e3, splits))
+        del g
+
+    def fit(ys):
+        xs = [p[1] for p in pts]
+        n = len(xs)
+        mx, my = sum(xs) / n, sum(ys) / n
+        b = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+        return b, my - b * mx  # us per byte, us at zero bytes
+
+    bl, al = fit([p[2] for p in pts])
+    bk, ak = fit([p[3] for p in pts])
+    return {
+        "points": [{"n_kv": p[0], "splits": p[4], "per_layer_us": round(p[2], 2), "fa_decode_us": round(p[3], 2)}
+                   for p in pts],
+        "layer_marginal_GB/s": round(1e-3 / bl, 1),
+        "layer_fixed_us": round(al, 2),
+        "fa_decode_marginal_GB/s": round(1e-3 / bk, 1),
+        "fa_decode_marginal_frac_of_peak": round(1e-3 / bk / HBM_PEAK_GBS, 4),
+        "fa_decode_fixed_us": round(ak, 2),
+        "timing": "per layer: HIP graph replay of the 10-layer step; fa_decode: events, eager; "
+                  "least-squares line over the points",
+        "rounds": rounds}
 
 
 def prefill_flops(n_q, start, heads=H, head_dim=D):
@@ -662,6 +724,8 @@ def main():
         result["decode_graph_replay"] = {"per_layer_us": round(ms_g * 1e3 / N_LAYERS, 2),
                                          "GB/s": round(bytes_step / (ms_g * 1e-3) / 1e9, 1)}
         del graph
+        if n_main == N_KV:
+            result["decode_length_curve"] = length_curve_leg(sqa, torch, dev, ks, vs, max(10, args.steps))
 
     if not args.no_verify:
         result["verify_nq2"] = verify_leg(sqa, torch, dev, ks, vs, args.steps,
