@@ -15,6 +15,15 @@ constexpr int kHeadDim = 256;
 constexpr int kBlocksPerHead = kHeadDim / SQA_QK4_0;            // 8
 constexpr int kHeadRowBytes = kBlocksPerHead * SQA_Q4_0_BLOCK_BYTES;  // 144
 
+// Store of an attention kernel's result or split partial, written through to
+// memory at once (an agent-scope relaxed store: a vector store with sc1). The
+// next kernel reads it from memory anyway (the L2 of another XCD cannot serve
+// it), and a plain store leaves a dirty L2 line that the end of the kernel must
+// write back, after the last workgroup's stores, on the critical path.
+__device__ __forceinline__ void store_through(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Records a message for sqa_last_error() and returns the status.
 int set_error(int status, const char *fmt, ...);
 int hip_status(hipError_t e, const char *what);

@@ -618,8 +618,8 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             const float L = (lbuf[my_r] + lbuf[16 + my_r]) + (lbuf[32 + my_r] + lbuf[48 + my_r]);
             const int tq = my_r / p.G, hq = kvh * p.G + my_r % p.G;
             const int64_t ridx = (int64_t)split * rows_total + (int64_t)tq * p.H + hq;
-            p.part_ml[ridx * 2 + 0] = m_ref == -INFINITY ? m_ref : m_ref * kLn2;  // combine works in base e
-            p.part_ml[ridx * 2 + 1] = L;
+            store_through(p.part_ml + ridx * 2 + 0, m_ref == -INFINITY ? m_ref : m_ref * kLn2);  // combine works in base e
+            store_through(p.part_ml + ridx * 2 + 1, L);
         }
     } else {
         // ============ value wavefronts: O[rows][64 dims] += P V =================
@@ -1001,8 +1001,8 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             float *dst = p.part_acc + ((int64_t)split * rows_total + (int64_t)tq * p.H + hq) * 256 + 64 * dq + n;
 #pragma unroll
             for (int bl = 0; bl < 2; ++bl) {
-                dst[32 * bl] = fmaf(acc[2 * bl][i], 16777216.0f, -8.0f * cor[bl][i]) * o_scale;
-                dst[32 * bl + 16] = fmaf(acc[2 * bl + 1][i], 1048576.0f, -8.0f * cor[bl][i]) * o_scale;
+                store_through(dst + 32 * bl, fmaf(acc[2 * bl][i], 16777216.0f, -8.0f * cor[bl][i]) * o_scale);
+                store_through(dst + 32 * bl + 16, fmaf(acc[2 * bl + 1][i], 1048576.0f, -8.0f * cor[bl][i]) * o_scale);
             }
         };
         if (!TWO) {

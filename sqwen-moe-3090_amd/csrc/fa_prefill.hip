@@ -905,18 +905,18 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
                                                                          hrow * p.gate_nb1)[16 * T + n];
                         o = o * (1.0f / (1.0f + expf(-gv)));
                     }
-                    p.dst[ridx * kHeadDim + 16 * T + n] = o;
+                    store_through(p.dst + ridx * kHeadDim + 16 * T + n, o);
                 }
             } else {
                 float *pa_out = p.part_acc + ((int64_t)split * rows_total + ridx) * kHeadDim;
 #pragma unroll
-                for (int T = 0; T < 16; ++T) pa_out[16 * T + n] = acc[rg][T][i];
+                for (int T = 0; T < 16; ++T) store_through(pa_out + 16 * T + n, acc[rg][T][i]);
                 if (n == 0) {
                     // the combine works in base e: m * ln 2 (acc and l of every split
                     // carry the same 2^ep, which cancels in the merge)
-                    p.part_ml[((int64_t)split * rows_total + ridx) * 2] =
-                        mrow == -INFINITY ? mrow : mrow * 0.6931471805599453f;
-                    p.part_ml[((int64_t)split * rows_total + ridx) * 2 + 1] = lrow;
+                    store_through(p.part_ml + ((int64_t)split * rows_total + ridx) * 2,
+                                  mrow == -INFINITY ? mrow : mrow * 0.6931471805599453f);
+                    store_through(p.part_ml + ((int64_t)split * rows_total + ridx) * 2 + 1, lrow);
                 }
             }
         }
