@@ -165,9 +165,10 @@ def test_decode_is_deterministic(sqa, orc, dev):
     assert np.array_equal(a, b)
 
 
-@pytest.mark.parametrize("n_q,n_kv", [(1, 172032), (2, 131072)])
+@pytest.mark.parametrize("n_q,n_kv", [(1, 172032), (2, 131072), (1, 262144)])
 def test_full_size_against_oracle(sqa, orc, dev, n_q, n_kv):
-    """Decode at 172K context and verify at 128K, the long-context shapes."""
+    """Decode at 172K context and verify at 128K, the long-context shapes, and
+    decode at 262144 keys (16 tiles per split, past the bench's 10.5)."""
     q, kq, vq = qkv(orc, 23 + n_q, n_q, n_kv)
     mask = orc.causal_mask(n_q, n_kv, n_kv - n_q)
     ref = orc.flash_attn_ext(q, kq, vq, mask)
