@@ -11,12 +11,13 @@
 //   on the same XCD (so the cache lines the heads share in a cache row of
 //   Hkv x 144 bytes are fetched from HBM once and served to the other heads'
 //   workgroups by that XCD's L2); two workgroups fit on a CU, so one's
-//   wavefronts can issue while the other's wait at their barrier. Of the two workgroups on a CU the one
-//   dispatched first wins the issue arbitration (older wavefronts go first)
-//   and runs about twice as fast while both are resident, so the splits of
-//   the first dispatch round take twice the tiles of the second: both rounds
-//   then end together (measured at 172K keys: 27.0 us against 28.6 us for
-//   equal splits, whose second round runs on alone for the last tiles). A workgroup (8 wavefronts) walks its split
+//   wavefronts can issue while the other's wait at their barrier. Of the two
+//   workgroups on a CU the one dispatched first wins the issue arbitration
+//   (older wavefronts go first) and runs about twice as fast while both are
+//   resident, so the splits of the first dispatch round take twice the tiles
+//   of the second: both rounds then end together (measured at 172K keys: 27.0
+//   us against 28.6 us for equal splits, whose second round runs on alone for
+//   the last tiles). A workgroup (8 wavefronts) walks its split
 //   in 64-key tiles: four score wavefronts (16-key quarter w of every tile)
 //   compute the logits and the softmax weights P of tile t; four value
 //   wavefronts (64-dim slice v of the output) accumulate P V of tile t-1 over
@@ -65,13 +66,18 @@
 //     exactly). P is kept at 2^-4 of its value (<= 16); 2^E is one power of
 //     two per value wavefront that puts the largest |d_v| it has seen near 2^8
 //     (lowered, with O rescaled, when a larger one comes), so A stays finite
-//     and clear of fp16 subnormals for V of any size.
+//     and clear of fp16 subnormals for V of any size. With up to 8 query rows,
+//     A rows 8-15 carry the lo parts of rows 0-7, so one set of three MFMAs
+//     per half tile and block serves both parts (C rows r and r + 8 are added
+//     at the end).
 //   * A key that no row of the call sees (masked in every row, past the split
 //     or past the cache end) contributes exactly 0 whatever its bytes, as in
 //     ggml's CPU loop, which skips masked keys: a -inf mask entry replaces the
 //     logit, and the score wavefronts publish which keys have P != 0 in some
 //     row, so the value wavefronts zero the others' V scales.
-//   * Splits are merged by fa_combine (fa_combine.hip).
+//   * Splits are merged by fa_combine (fa_combine.hip). The partials are
+//     written through to memory (store_through), so the end of the kernel has
+//     no dirty L2 lines of them to write back.
 //
 // MFMA operand layouts (lane = 16*g + n):
 //   16x16x64 i8 : A[n][16g..16g+15]  B[16g..16g+15][n]  C[4g..4g+3][n]
