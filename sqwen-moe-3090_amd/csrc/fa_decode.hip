@@ -58,10 +58,13 @@
 //     to spare for it (two workgroups per CU need <= 128 VGPRs).
 //   * PV: v_mfma_f32_16x16x32_f16 with fp32 accumulation, d_v on the A side:
 //     A = P d_v 2^E of the block as an exact fp16 hi + lo pair (P arrives as an
-//     fp16 hi + lo pair, ~22 bits), B = the raw nibbles as fp16 subnormals (nib
-//     * 2^-24, or nib * 2^-20 for the high nibble, one v_and per two keys), and
-//     the -8 offset as -8 * sum A from one more MFMA against ones. Every product
-//     is exact in fp32, so a row that a few keys dominate carries no fp16
+//     fp16 hi + lo pair, ~22 bits), B = the nibbles: one v_and per two keys
+//     leaves the fp16 subnormal nib * 2^-24 for the low nibble, which one packed
+//     multiply by 2^14 lifts to nib * 2^-10 (as a subnormal 2^-24 deep, the
+//     MFMA's fp32 sums lost up to ~2^-12 of the output at long contexts), and nib
+//     * 2^-20 for the high nibble; the -8 offset comes in as -8 * sum A from one
+//     more MFMA against ones. Every product is exact in fp32, so a row
+//     that a few keys dominate carries no fp16
 //     rounding of V or P into its output (ggml's CPU path dequantizes V to fp32
 //     exactly). P is kept at 2^-4 of its value (<= 16); 2^E is one power of
 //     two per value wavefront that puts the largest |d_v| it has seen near 2^8
@@ -742,10 +745,12 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
         }
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // Q operands published
         const int dq = wq;  // dims 64dq..64dq+63: blocks 2dq, 2dq+1
-        // B operand straight from the nibbles: a nibble in the low bits of an fp16
-        // is the subnormal nib * 2^-24 (low nibble) or, left in bits 4-7,
-        // nib * 2^-20 (high nibble), exact values that the MFMA multiplies exactly.
+        // B operand from the nibbles: a nibble in the low bits of an fp16 is the
+        // subnormal nib * 2^-24 (low nibble), which one packed multiply by 2^14
+        // makes nib * 2^-10, exact and normal; left in bits 4-7, the high nibble
+        // is nib * 2^-20 and enters as it is.
         const half8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+        const half8 kLoToNormal = {16384, 16384, 16384, 16384, 16384, 16384, 16384, 16384};  // 2^14
         uint8_t *dv_comp = smem + kOffDv + vw * 256;  // [bl][half][g][j] fp16
         const int ra = n & kRowMask;  // P row of this lane's A operand
         // d_v compaction: lane -> block bl, half h, key group gg, pair jj: keys
@@ -767,9 +772,10 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             vsel[bl] = b | (0x0cu << 8) | ((4u + b) << 16) | (0x0cu << 24);
         }
 
-        // acc[2bl] = 2^-24 sum_k A nib_lo, acc[2bl + 1] = 2^-20 sum_k A nib_hi, and
+        // acc[2bl] = 2^-10 sum_k A nib_lo, acc[2bl + 1] = 2^-20 sum_k A nib_hi, and
         // cor[bl] = sum_k A, with A = P d_v of block 2dq + bl, so that
-        // O[row 4g+i][dim 64dq + 32bl + n (+16 for the high nibble)] = 2^24 acc - 8 cor.
+        // O[row 4g+i][dim 64dq + 32bl + n] = 2^10 acc - 8 cor (2^20 acc for the
+        // high nibble, dim + 16).
         floatx4 acc[4], cor[2];
 #pragma unroll
         for (int T = 0; T < 4; ++T) acc[T] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -975,6 +981,11 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                     half8 blo, bhi;
                     __builtin_memcpy(&blo, wlo, 16);
                     __builtin_memcpy(&bhi, whi, 16);
+                    // nib 2^-24 times 2^14: nib 2^-10 exactly, in the normal range (with
+                    // the low nibbles as subnormals 2^-24 deep, the MFMA's sums lost up
+                    // to ~2^-12 of the output at long contexts; the high nibbles' nib
+                    // 2^-20 cost nothing measurable)
+                    blo = blo * kLoToNormal;
                     if (TWO) {
                         const half8 ah = pa[h] * dv8;
                         const half8 ar = __builtin_elementwise_fma(pa[h], dv8, -ah);
@@ -1007,7 +1018,7 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
             float *dst = p.part_acc + ((int64_t)split * rows_total + (int64_t)tq * p.H + hq) * 256 + 64 * dq + n;
 #pragma unroll
             for (int bl = 0; bl < 2; ++bl) {
-                store_through(dst + 32 * bl, fmaf(acc[2 * bl][i], 16777216.0f, -8.0f * cor[bl][i]) * o_scale);
+                store_through(dst + 32 * bl, fmaf(acc[2 * bl][i], 1024.0f, -8.0f * cor[bl][i]) * o_scale);
                 store_through(dst + 32 * bl + 16, fmaf(acc[2 * bl + 1][i], 1048576.0f, -8.0f * cor[bl][i]) * o_scale);
             }
         };

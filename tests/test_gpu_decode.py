@@ -186,7 +186,10 @@ def test_long_context_outliers_against_f64(sqa, orc, dev, n_q):
     every relative error there, and ggml's own fp32 CPU path (the oracle) lands
     up to ~3.4e-3 x RMS from the exact result at such lengths (2.6e-3 for n_q=1
     here, 2.8e-4 for n_q=2: it depends on the data). The kernel is checked
-    against a float64 brute force on the same dequantized operands instead."""
+    against a float64 brute force on the same dequantized operands instead, at
+    a bound a quarter of the tolerance: with the low nibbles of V as fp16
+    subnormals in the PV MFMA it read 1.1e-3 here, with them lifted into the
+    normal range ~1e-4."""
     n_kv = 172032
     q, kq, vq = qkv(orc, 5 + n_q, n_q, n_kv, outliers=5)
     mask = orc.causal_mask(n_q, n_kv, n_kv - n_q)
@@ -196,7 +199,7 @@ def test_long_context_outliers_against_f64(sqa, orc, dev, n_q):
                                  fa_ref.cache_dequant(orc, vq), 1 / 16, mask)
     e_gpu, e_orc = rel_err(got, exact), rel_err(ref, exact)
     print(f"n_q={n_q}: gpu vs f64 {e_gpu:.3e}, oracle vs f64 {e_orc:.3e}, gpu vs oracle {rel_err(got, ref):.3e}")
-    assert e_gpu <= TOL
+    assert e_gpu <= TOL / 4
 
 
 @pytest.mark.parametrize("n_kv", [1, 2, 17, 40])
