@@ -34,9 +34,10 @@
 //     with A = P d_v as an fp16 hi + lo pair built by packed fp16 ops (two
 //     MFMAs, ~22 bits) and B = the exact V codes, so every product is exact in
 //     fp32. P carries 2^ep, one power of two per KV head (the largest |d_v| of
-//     the head brought toward [1, 2), ep clamped to [-6, 7] so that P stays
-//     finite): it keeps A clear of fp16 subnormals and overflow for every
-//     |d_v| < 16376, and l, summed from the same P, carries the same factor.
+//     the head brought toward [1, 2), but P 2^ep held at or above P where A's
+//     range allows, ep in [-6, 7]): it keeps P and A clear of fp16 subnormals
+//     and overflow for every |d_v| < 16376, and l, summed from the same P,
+//     carries the same factor.
 //     The d_v and V operands of a tile are read ahead of the MFMAs that use them.
 //   A masked key contributes exactly 0 even over NaN/Inf block scales (as ggml's
 //   CPU loop, which skips it): a -inf mask entry replaces the logit, and the
@@ -556,11 +557,15 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
             e2 = 1 - e < 15 ? 1 - e : 15;
         }
     }
-    // 2^ep with ep = e2 clamped to [-6, 7] rides on P (the score waves' exp2
-    // argument): P 2^ep <= 2^(kSlack + 7) stays finite in fp16 and A = P 2^ep d_v
-    // below 2^9 for max |d_v| in [2^-8, 2^7), below 65504 for every |d_v| < 16376.
-    // O and l both carry it, so it cancels in O / l.
-    const int ep = e2 < -6 ? -6 : (e2 > 7 ? 7 : e2);
+    // 2^ep rides on P (the score waves' exp2 argument); O and l both carry it,
+    // so it cancels in O / l. ep = e2 (at most 7) while that is not negative;
+    // below, ep = min(e2 + 5, 0), at least -6: P 2^ep <= 2^(kSlack + 7) stays
+    // finite in fp16, A = P 2^ep d_v stays below 2^14 for max |d_v| < 2^12 and
+    // below 65504 for every |d_v| < 16376, and P 2^ep is not pushed toward the
+    // fp16 subnormals further than A's range requires. (ep = e2 alone put the P
+    // of keys a few binades below the row maximum into the subnormals for large
+    // V, max |d_v| ~ 50: outputs up to 3e-3 x RMS from the exact result.)
+    const int ep = e2 >= 0 ? (e2 > 7 ? 7 : e2) : (e2 + 5 < -6 ? -6 : (e2 + 5 > 0 ? 0 : e2 + 5));
     const int nh = (n >> 3) & 1;
 
     // The two kinds of wave run separate code with the same barrier count:

@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 import torch
 
+from tests import fa_ref
 from tests.gen import qkv, rel_err
 from tests.test_gpu_decode import run_gpu
 
@@ -120,6 +121,25 @@ def test_prefill_v_scale_range(sqa, orc, dev, scale_v):
     dv = np.abs(vq.reshape(-1, 18)[:, :2].copy().view(np.float16)).max()
     print(f"prefill V x{scale_v} (max |d_v| {dv:.3g}): max err / rms = {err:.3e}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("seed", [100, 101])
+def test_prefill_large_v_outliers_against_f64(sqa, orc, dev, seed):
+    """Large V (x17.7, 8 outlier channels x8: max |d_v| about 50) over 3 KV
+    heads of 16 query heads. The weight of P on 2^ep must not push the P of keys
+    a few binades below the row maximum into the fp16 subnormals (ep = e2 did:
+    3e-4 to 1.1e-3 x RMS from the exact result over these seeds); measured
+    against a float64 brute force on the dequantized operands, as ggml's fp32
+    CPU path is itself ~1e-3 off here."""
+    n_q, n_kv = 40, 2807
+    q, kq, vq = qkv(orc, seed, n_q, n_kv, H=48, Hkv=3, outliers=8, scale_v=17.7)
+    mask = orc.causal_mask(n_q, n_kv, n_kv - n_q)
+    got = run_gpu(sqa, dev, q, kq, vq, mask)
+    exact = fa_ref.attention_f64(fa_ref.q8_dequant(orc, q), fa_ref.cache_dequant(orc, kq),
+                                 fa_ref.cache_dequant(orc, vq), 1 / 16, mask)
+    err = rel_err(got, exact)
+    print(f"large V seed {seed}: gpu vs f64 {err:.3e}")
+    assert err <= TOL / 10
 
 
 def test_prefill_masked_rows_with_garbage_bytes(sqa, orc, dev):
