@@ -163,8 +163,7 @@ int sqa_supports_rope_norm(const sqa_tensor *dst, const sqa_tensor *src, const s
  * kernel; larger n_q uses the MFMA prefill kernel.
  * Inputs: a key that -inf excludes from every row of the call contributes 0
  * whatever its bytes hold (stale or unwritten cache rows may be anything);
- * V block scales |d_v| < 16376 for the prefill kernel (any finite size for
- * decode/verify). A row with no visible key returns 0.
+ * V block scales of any finite size. A row with no visible key returns 0.
  */
 int sqa_flash_attn_ext(const sqa_tensor *q, const sqa_tensor *k, const sqa_tensor *v,
                        const sqa_tensor *mask, float scale, float max_bias, float logit_softcap,

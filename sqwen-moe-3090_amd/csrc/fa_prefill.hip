@@ -26,18 +26,17 @@
 //     fp32: a code has at most 3 significant bits) and the d_k scaling as an
 //     fp32 FMA with the fp16 scale as operand; then the mask and the
 //     online softmax in fp32 (base 2, with a lazy reference maximum that moves
-//     only when a logit passes it by more than 2^8, so P <= 2^8 and most tiles
-//     need no rescale of O). P (as an fp16 hi + lo pair) and the rescale
-//     factors go to LDS.
+//     only when a logit passes it by more than a slack of ks binades, so
+//     P <= 2^ks and most tiles need no rescale of O; ks = 8 unless V is large,
+//     below). P (as an fp16 hi + lo pair) and the rescale factors go to LDS.
 //   value wave 4 + w, the same 32 rows, holds their O (128 registers) one tile
 //     behind: O = alpha O + P V per block b (alpha only when a maximum moved)
 //     with A = P d_v as an fp16 hi + lo pair built by packed fp16 ops (two
 //     MFMAs, ~22 bits) and B = the exact V codes, so every product is exact in
-//     fp32. P carries 2^ep, one power of two per KV head (the largest |d_v| of
-//     the head brought toward [1, 2), but P 2^ep held at or above P where A's
-//     range allows, ep in [-6, 7]): it keeps P and A clear of fp16 subnormals
-//     and overflow for every |d_v| < 16376, and l, summed from the same P,
-//     carries the same factor.
+//     fp32. P carries 2^ep, one power of two per KV head, and l, summed from
+//     the same P, carries the same factor. ep and ks follow the largest |d_v|
+//     of the head so that A = P 2^ep d_v stays below 2^15 for every finite V
+//     while P 2^ep stays as far from the fp16 subnormals as that allows.
 //     The d_v and V operands of a tile are read ahead of the MFMAs that use them.
 //   A masked key contributes exactly 0 even over NaN/Inf block scales (as ggml's
 //   CPU loop, which skips it): a -inf mask entry replaces the logit, and the
@@ -92,7 +91,7 @@ constexpr int kLdsA = kLdsP + 2 * kPBuf;          // [4 waves][2 rg][16 rows] f3
 constexpr int kABuf = kScoreWaves * kRG * 16 * 4;
 constexpr int kLdsMask = kLdsA + 2 * kABuf;       // [qb positions][32 keys] f16
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kSlack = 8.0f;  // log2 of the largest P the lazy rescale admits
+constexpr int kSlack = 8;  // log2 of the largest P the lazy rescale admits (V not large)
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 static_assert(kTileBytes == 33792 && kTileBytes % 256 == 0, "tile record");
@@ -558,14 +557,22 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
         }
     }
     // 2^ep rides on P (the score waves' exp2 argument); O and l both carry it,
-    // so it cancels in O / l. ep = e2 (at most 7) while that is not negative;
-    // below, ep = min(e2 + 5, 0), at least -6: P 2^ep <= 2^(kSlack + 7) stays
-    // finite in fp16, A = P 2^ep d_v stays below 2^14 for max |d_v| < 2^12 and
-    // below 65504 for every |d_v| < 16376, and P 2^ep is not pushed toward the
-    // fp16 subnormals further than A's range requires. (ep = e2 alone put the P
-    // of keys a few binades below the row maximum into the subnormals for large
-    // V, max |d_v| ~ 50: outputs up to 3e-3 x RMS from the exact result.)
-    const int ep = e2 >= 0 ? (e2 > 7 ? 7 : e2) : (e2 + 5 < -6 ? -6 : (e2 + 5 > 0 ? 0 : e2 + 5));
+    // so it cancels in O / l. The lazy rescale keeps P 2^ep <= 2^(ks + ep), and
+    // |d_v| < 2^(1 - e2), so A = P 2^ep d_v < 2^(ks + ep + 1 - e2):
+    //   e2 >= 0: ep = e2 (at most 7), ks = 8: A < 2^9, P 2^ep <= 2^15;
+    //   e2 < 0: ks + ep = 14 + e2 (A < 2^15), ep = 0 while ks can give way
+    //     (down to 3), then ep < 0 (to -4 at fp16's largest d_v).
+    // Lowering ep instead (ep = e2 for large V, max |d_v| >= 2) put the P of keys
+    // a few binades below the row maximum into the fp16 subnormals, where its
+    // lo half vanishes: outputs up to 3e-3 x RMS from the exact result. A smaller
+    // slack only moves the reference maximum more often.
+    int ep = e2 > 7 ? 7 : e2, ks = kSlack;
+    if (e2 < 0) {
+        const int top = 14 + e2;  // log2 of the largest P 2^ep that A's range admits
+        ks = top >= kSlack ? kSlack : (top >= 3 ? top : 3);
+        ep = top >= 3 ? 0 : top - 3;
+    }
+    const float lim_top = (float)(ks + ep);  // the lazy test's bound on s'
     const int nh = (n >> 3) & 1;
 
     // The two kinds of wave run separate code with the same barrier count:
@@ -581,8 +588,8 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
         // The logits are accumulated relative to the row's P reference mref =
         // (m_run, or 0 before the first visible key) - ep: s' = s - mref, so that
         // P = 2^s' needs no subtraction, and the lazy-maximum test s > m_run +
-        // kSlack reads s' > lim_s (kSlack + ep, or -inf before the first visible
-        // key). Both change only when the maximum moves.
+        // ks reads s' > lim_s (ks + ep, or -inf before the first visible key).
+        // Both change only when the maximum moves.
         float mref[kRG], lim_s[kRG];
 #pragma unroll
         for (int rg = 0; rg < kRG; ++rg) {
@@ -734,7 +741,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
 #pragma unroll
             for (int rg = 0; rg < kRG; ++rg) {
                 // lazy maximum: the reference moves only when a logit passes it by more
-                // than kSlack, so P <= 2^kSlack and most tiles need no rescale of O
+                // than ks, so P <= 2^ks and most tiles need no rescale of O
                 float alpha = 1.0f;
                 bool over = false;
 #pragma unroll
@@ -754,7 +761,7 @@ __global__ __launch_bounds__(kThreads, 1) void fa_prefill_kernel(PrefillParams p
 #pragma unroll
                     for (int jj = 0; jj < 8; ++jj) s[rg][jj] += d;
                     mref[rg] = mref_new;
-                    lim_s[rg] = m_new == -INFINITY ? -INFINITY : kSlack + (float)ep;
+                    lim_s[rg] = m_new == -INFINITY ? -INFINITY : lim_top;
                 }
                 float pf[8], psum = 0.0f;
 #pragma unroll

@@ -83,9 +83,10 @@ def test_rising_logits_force_rescales(sqa, orc, dev, n_q):
 
 
 @pytest.mark.parametrize("H,Hkv,n_q", [(4, 2, 6), (4, 1, 1), (8, 4, 3), (16, 2, 5)])
-def test_small_chunks_outside_the_decode_kernel(sqa, orc, dev, H, Hkv, n_q):
-    """Shapes the split-KV decode kernel does not take (more than 4 positions,
-    or n_head_kv != 2) run as prefill chunks, whatever their row count."""
+def test_small_chunks_at_other_gqa_ratios(sqa, orc, dev, H, Hkv, n_q):
+    """Up to 4 positions with at most 16 query rows per KV head run on the
+    split-KV decode kernel whatever n_head_kv is ((4, 1, 1), (8, 4, 3)); more
+    positions run as prefill chunks whatever their row count."""
     q, kq, vq = qkv(orc, 31 + n_q, n_q, 700, H=H, Hkv=Hkv)
     mask = orc.causal_mask(n_q, 700, 700 - n_q)
     ref = orc.flash_attn_ext(q, kq, vq, mask)
@@ -107,12 +108,13 @@ def test_chunk_at_context_start_with_outliers(sqa, orc, dev, n_q, n_kv, start):
     assert err <= TOL
 
 
-@pytest.mark.parametrize("scale_v", [1e-4, 3e-2, 500.0, 2000.0])
+@pytest.mark.parametrize("scale_v", [1e-4, 3e-2, 500.0, 2000.0, 8000.0])
 def test_prefill_v_scale_range(sqa, orc, dev, scale_v):
-    """V of any size the kernel admits (|d_v| < 16376): the softmax weights carry
-    2^ep, ep from the largest |d_v| of the head clamped to [-6, 7], so that P d_v
-    keeps 22 bits without overflow; 1e-4 and 500 reach the two ends of the clamp,
-    2000 (|d_v| about 5000 on the outlier channels) nears the overflow bound."""
+    """V of any finite size: the softmax weights carry 2^ep and the lazy rescale
+    a slack of ks binades, both from the largest |d_v| of the head, so that
+    P d_v keeps 22 bits without overflow. 1e-4 reaches ep = 7; 500 (largest
+    |d_v| about 1800, on the outlier channels) a slack of 4 with ep = 0; 2000
+    and 8000 (|d_v| about 7400 and 29500) ep = -1 and -3 with a slack of 3."""
     q, kq, vq = qkv(orc, 77, 300, 512, outliers=5, scale_v=scale_v)
     mask = orc.causal_mask(300, 512, 212)
     ref = orc.flash_attn_ext(q, kq, vq, mask)
