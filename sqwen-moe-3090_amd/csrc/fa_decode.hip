@@ -932,11 +932,21 @@ __global__ __launch_bounds__(kThreads, TWO ? 2 : 4) void fa_decode_kernel(Decode
                 for (int h = 0; h < 2; ++h) {
                     const half8 ph = *reinterpret_cast<const half8 *>(prow + 32 * h);
                     const half8 plo = *reinterpret_cast<const half8 *>(prow + 64 + 32 * h);
+                    // P alpha as hi = fp16(P alpha) and lo = fp16(P alpha - hi), both
+                    // rounded once from the exact product by v_fma_mixlo_f16. Left to
+                    // the compiler, the stored hi came from the fp32 product (rounded
+                    // twice) and the hi subtracted for lo from the exact one, and where
+                    // the product sat near an fp16 rounding midpoint the two differed:
+                    // hi + lo one fp16 ulp of hi off.
+                    const float al = exp2_or_zero(mw[2 * h + (g >> 1)], mna);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        const float xv = ((float)ph[e] + (float)plo[e]) * exp2_or_zero(mw[2 * h + (g >> 1)], mna);
-                        const _Float16 hi = (_Float16)xv;
-                        const _Float16 lo = (_Float16)(xv - (float)hi);
+                        const float sv = (float)ph[e] + (float)plo[e];  // exact: lo is below hi's ulp
+                        uint32_t hw, lw;
+                        asm("v_fma_mixlo_f16 %0, %1, %2, 0" : "=v"(hw) : "v"(sv), "v"(al));
+                        asm("v_fma_mixlo_f16 %0, %1, %2, -%3 op_sel_hi:[0,0,1]" : "=v"(lw) : "v"(sv), "v"(al), "v"(hw));
+                        const _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)hw);
+                        const _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)lw);
                         pa[h][e] = TWO || n < 8 ? hi : lo;
                         pl[h][e] = TWO ? lo : (n < 8 ? (_Float16)0 : hi);
                     }

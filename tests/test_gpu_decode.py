@@ -202,6 +202,26 @@ def test_long_context_outliers_against_f64(sqa, orc, dev, n_q):
     assert e_gpu <= TOL / 4
 
 
+def test_rescaled_first_tile_against_f64(sqa, orc, dev):
+    """16-row form (3 positions x 4 heads per KV head, 8 KV heads, 2533 keys,
+    8 outlier channels): every split's first tile is rescaled from the score
+    wavefronts' own maxima onto their common one, as an fp16 hi + lo pair of
+    P alpha. With the product left visible to the compiler, the stored hi and
+    the hi subtracted for lo were rounded apart (once from the fp32 product,
+    once from the exact one), and where the product sat on an fp16 rounding
+    midpoint hi + lo came out one ulp of hi high: here key 1480 of row (2, 20),
+    1.06e-3 x RMS from the float64 result through an outlier channel of V."""
+    n_q, n_kv = 3, 2533
+    q, kq, vq = qkv(orc, 709755409, n_q, n_kv, H=32, Hkv=8, outliers=8, scale_v=8.405397906523204)
+    mask = orc.causal_mask(n_q, n_kv, n_kv - n_q)
+    got = run_gpu(sqa, dev, q, kq, vq, causal=n_kv - n_q)
+    exact = fa_ref.attention_f64(fa_ref.q8_dequant(orc, q), fa_ref.cache_dequant(orc, kq),
+                                 fa_ref.cache_dequant(orc, vq), 1 / 16, mask)
+    err = rel_err(got, exact)
+    print(f"rescaled first tiles: gpu vs f64 {err:.3e}")
+    assert err <= TOL / 10
+
+
 @pytest.mark.parametrize("n_kv", [1, 2, 17, 40])
 def test_few_visible_keys_with_outliers(sqa, orc, dev, n_kv):
     """A row that a few keys dominate: its output is a handful of V rows, so an
