@@ -3,8 +3,10 @@
 Every source is compiled by hipcc (-x hip) into _build/, then linked into a
 shared library next to this file. Flags:
   -Xclang -target-feature -Xclang -packed-fp32-ops   no packed fp32 VALU ops
-  -ffp-contract=fast-honor-pragmas is hipcc's default; kernels that must not
-  contract use explicit __fmul_rn/__fadd_rn.
+  -ffp-contract=fast-honor-pragmas is hipcc's default; code that must round
+  every multiply and add on its own (the q4_0 quantizer, the K/Q producer)
+  says #pragma clang fp contract(off): HIP's __fmul_rn/__fadd_rn are plain
+  * and + and do not stop the fusion.
 """
 import concurrent.futures
 import glob

@@ -4,7 +4,7 @@
 //   d    = max / -8            (stored as fp16, round-to-nearest-even)
 //   id   = d != 0 ? 1/d : 0    (correctly rounded fp32 division)
 //   code = min(15, (int8_t)(x*id + 8.5f)) with the multiply and the add each
-//          rounded on their own (no fused multiply-add)
+//          rounded on their own (contraction off: no fused multiply-add)
 // An all-zero block therefore stores d = -0.0 (fp16 0x8000) and codes 8.
 #pragma once
 #include "common.hpp"
@@ -14,6 +14,11 @@ namespace sqa {
 // v: this lane's 4 values (block elements 4t..4t+3, t = lane & 7); blk: the
 // 18-byte block. All 8 lanes of the group must call it together.
 __device__ __forceinline__ void quantize_q4_0_block8(const float v[4], int t, uint8_t *blk) {
+    // x*id + 8.5f as two roundings: with contraction on (hipcc's default, and
+    // inside HIP's __fmul_rn / __fadd_rn, which are plain * and +) it became one
+    // fma (v_fmaak_f32), and a value whose x*id lies within half an ulp below a
+    // half-integer then truncated to the code below ggml's
+#pragma clang fp contract(off)
     // Lane-local first-occurrence maximum of |x|; index 32 marks "none".
     float amax = 0.0f, mx = 0.0f;
     int im = 32;
@@ -35,7 +40,7 @@ __device__ __forceinline__ void quantize_q4_0_block8(const float v[4], int t, ui
     uint32_t word = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const float y = __fadd_rn(__fmul_rn(v[j], id), 8.5f);
+        const float y = v[j] * id + 8.5f;
         int c = (int)y;  // truncation toward zero, y in [0.5, 16.5] for finite input
         c = c < 15 ? c : 15;
         word |= (uint32_t)(c & 0xff) << (8 * j);

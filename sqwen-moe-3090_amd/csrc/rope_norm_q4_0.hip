@@ -7,14 +7,14 @@
 // kernels with the rows round-tripping through memory between them.
 //
 // Arithmetic follows ggml's CPU kernels step by step, each operation rounded on
-// its own:
+// its own (contraction off in the kernel):
 //   norm: sum of x*x in double, mean = (float)(sum / D), scale =
-//         1/sqrtf(mean + eps), y = x*scale, then y*w;
+//         1/sqrtf(mean + eps) (the root correctly rounded), y = x*scale, then y*w;
 //   rope: the angle of rotation pair ic is the token's position of the pair's
 //         IMROPE sector times theta_scale^ic, formed as ic successive fp32
 //         multiplies (theta_scale = powf(freq_base, -2/n_rot) is computed once on
 //         the host with the C library, as ggml does); cos/sin of freq_scale*angle
-//         times attn_factor; (x0, x1) = (y[ic], y[ic + n_rot/2]) ->
+//         (correctly rounded) times attn_factor; (x0, x1) = (y[ic], y[ic + n_rot/2]) ->
 //         (x0*c - x1*s, x0*s + x1*c); dims >= n_rot pass through;
 //   q4_0: ggml's quantize_row_q4_0_ref (q4_0_block.hpp).
 //
@@ -53,6 +53,11 @@ struct ProducerParams {
 
 template <int D, bool kQ4, bool kVec>
 __global__ __launch_bounds__(kThreads) void rope_norm_kernel(ProducerParams p) {
+    // every multiply and add rounded on its own, as ggml's C: with contraction on
+    // (hipcc's default, and inside HIP's __fmul_rn / __fadd_rn, which are plain
+    // * and +) the rotation x0*c - x1*s became an fma, an ulp off in a quarter
+    // of the values
+#pragma clang fp contract(off)
     constexpr int kLanes = D / 4;                  // lanes per head row
     constexpr int kRowsPerPass = kThreads / kLanes;  // head rows in flight
     __shared__ float2 cs[D / 2];                   // (cos, sin) of rotation pair ic
@@ -70,11 +75,15 @@ __global__ __launch_bounds__(kThreads) void rope_norm_kernel(ProducerParams p) {
         else if (sector % 3 == 0 && sector < 3 * p.sections[0]) c = 0;
         else c = 3;
         float th = (float)p.pos[t + c * p.n_tok];
-        for (int k = 0; k < ic; ++k) th = __fmul_rn(th, p.theta_scale);
-        const float ang = __fmul_rn(p.freq_scale, th);
-        float sn, cn;
-        sincosf(ang, &sn, &cn);  // one argument reduction for both
-        cs[ic] = make_float2(__fmul_rn(cn, p.attn_factor), __fmul_rn(sn, p.attn_factor));
+        for (int k = 0; k < ic; ++k) th = th * p.theta_scale;
+        const float ang = p.freq_scale * th;
+        // cos and sin in double, rounded once to float: the correctly rounded
+        // values, which the C library's cosf/sinf also return but for about 1% of
+        // arguments (the fp32 device sincosf differs from them in the last bit far
+        // more often)
+        double sd, cd;
+        sincos((double)ang, &sd, &cd);
+        cs[ic] = make_float2((float)cd * p.attn_factor, (float)sd * p.attn_factor);
     }
     __syncthreads();
 
@@ -100,15 +109,19 @@ __global__ __launch_bounds__(kThreads) void rope_norm_kernel(ProducerParams p) {
         if (p.norm_w) {
             double s = 0.0;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) s += (double)__fmul_rn(v[j], v[j]);
+            for (int j = 0; j < 4; ++j) s += (double)(v[j] * v[j]);
 #pragma unroll
             for (int off = kLanes / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, kLanes);
             const float mean = (float)(s / (double)D);
-            const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, p.eps)));
+            // sqrtf correctly rounded, as the C library's: the root in double rounded
+            // once to float (the fp32 square root compiles to v_sqrt_f32 alone,
+            // up to an ulp off, which moved the scale of about 10% of rows)
+            const float root = (float)__builtin_sqrt((double)(mean + p.eps));
+            const float scale = __fdiv_rn(1.0f, root);
             const float4 w = *reinterpret_cast<const float4 *>(p.norm_w + 4 * l);
             const float wv[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] = __fmul_rn(__fmul_rn(v[j], scale), wv[j]);
+            for (int j = 0; j < 4; ++j) v[j] = v[j] * scale * wv[j];
         }
 
         float out[4];
@@ -120,10 +133,10 @@ __global__ __launch_bounds__(kThreads) void rope_norm_kernel(ProducerParams p) {
                 out[j] = v[j];
             } else if (d < half) {
                 const float2 c = cs[d];  // x0 = v, x1 = partner: x0*c - x1*s
-                out[j] = __fsub_rn(__fmul_rn(v[j], c.x), __fmul_rn(pv, c.y));
+                out[j] = v[j] * c.x - pv * c.y;
             } else {
                 const float2 c = cs[d - half];  // x0 = partner, x1 = v: x0*s + x1*c
-                out[j] = __fadd_rn(__fmul_rn(pv, c.y), __fmul_rn(v[j], c.x));
+                out[j] = pv * c.y + v[j] * c.x;
             }
         }
 

@@ -3,10 +3,15 @@ the GPU against the oracle's restatement of ggml's rms_norm -> mul ->
 rope_multi(IMROPE) -> set_rows chain (reference src/model/attn.rs:166-200,
 src/engine/kv.rs:313-399).
 
-Bar: the float stage (norm and rotation) agrees to a few fp32 ulps; the GPU's
-cosf/sinf and the C library's may differ in the last bit, so a q4_0 code may
-flip where the scaled value sits on a rounding boundary. Hence for the q4_0
-output: d (fp16) equal or one ulp apart, at least 99.9% of the codes equal, every
+Bar: the float stage (norm and rotation) agrees to a few fp32 ulps. The kernel's
+square root and cos/sin are correctly rounded; the C library's cosf/sinf are not
+for about 1% of arguments, so there the rotated value may differ in the last
+bit, and a q4_0 code may flip where the scaled value sits on a rounding boundary.
+Where two values of a block tie in magnitude to the last bit with opposite
+signs, the block maximum (the first of the largest, as ggml picks it) may be the
+other one: d changes sign and the codes mirror, which dequantises to the same
+values but the extreme one, a code step away. Hence for the q4_0 output: |d|
+(fp16) equal or one ulp apart, at least 99.9% of the codes equal, every
 dequantised value within one code step of the oracle's, and rows outside idx
 untouched. The quantizer itself is bit-exact (test_gpu_set_rows.py)."""
 import numpy as np
@@ -45,7 +50,7 @@ def _compare_q4(got, want, D):
     w = want.reshape(-1, 18)
     dg = g[:, :2].copy().view(np.uint16).ravel()
     dw = w[:, :2].copy().view(np.uint16).ravel()
-    assert _fp16_ulps(dg, dw).max() <= 1
+    assert _fp16_ulps(dg & 0x7FFF, dw & 0x7FFF).max() <= 1
     cg = np.concatenate([g[:, 2:] & 15, g[:, 2:] >> 4], axis=1)
     cw = np.concatenate([w[:, 2:] & 15, w[:, 2:] >> 4], axis=1)
     same = (cg == cw).mean()
