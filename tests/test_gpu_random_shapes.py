@@ -1,7 +1,8 @@
 """Seeded random shapes through the attention kernels against a float64 brute
 force, and through the K/Q producer against the oracle: KV heads 1-8, group
 sizes 1-16, decode / verify / prefill chunk sizes, causal-from-positions,
-causal and holed F16 masks, V scales over three decades, outlier channels.
+causal and holed F16 masks, the fused sigmoid gate, V scales over three
+decades, outlier channels.
 
 The float64 reference runs on the same dequantised operands (q8_0 Q, q4_0 K
 and V), so the bound measures the kernels' own arithmetic rather than ggml's
@@ -59,13 +60,20 @@ def test_random_attention_shapes_against_f64(sqa, orc, dev, seed):
         qt = torch.from_numpy(q).to(dev)
         kt = torch.from_numpy(np.ascontiguousarray(kq)).to(dev)
         vt = torch.from_numpy(np.ascontiguousarray(vq)).to(dev)
+        gate = None
         if form == "causal_pos":
-            out = sqa.flash_attn_ext_causal(qt, kt, vt, n_kv, n_kv - n_q, scale=1 / 16)
+            # half of these with the sigmoid gate fused (split merge or prefill epilogue)
+            gate = rng.standard_normal(q.shape).astype(np.float32) if rng.random() < 0.5 else None
+            gt = torch.from_numpy(gate).to(dev) if gate is not None else None
+            out = sqa.flash_attn_ext_causal(qt, kt, vt, n_kv, n_kv - n_q, gate=gt, scale=1 / 16)
         else:
             out = sqa.flash_attn_ext(qt, kt, vt, n_kv, mask=torch.from_numpy(mask).to(dev), scale=1 / 16)
         got = out.cpu().numpy()
         exact = fa_ref.attention_f64(fa_ref.q8_dequant(orc, q), fa_ref.cache_dequant(orc, kq),
                                      fa_ref.cache_dequant(orc, vq), 1 / 16, mask)
+        if gate is not None:
+            exact = exact / (1.0 + np.exp(-gate.astype(np.float64)))
+            label += " gate"
         err = rel_err(got, exact)
         worst = max(worst, err)
         assert np.all(np.isfinite(got)), label
