@@ -40,7 +40,7 @@ STACK_N_Q, STACK_START = 2048, 131072
 # passes over this script: 2.0 x FETCH_SIZE + 1.0 x WRITE_SIZE (KiB x 1024),
 # the factors taken from a plain 256 MiB copy in the same run
 # (profiles/fa_decode_verify_172k_pp512_out_proj_hbm_traffic.txt).
-DECODE_TRAFFIC_BYTES = int((2.0 * 48772.0 + 4160.0) * 1024)
+DECODE_TRAFFIC_BYTES = int((2.0 * 48758.8 + 4160.0) * 1024)
 H, HKV, D = 16, 2, 256
 N_LAYERS = 10
 N_KV = 172032
